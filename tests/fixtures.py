@@ -1,0 +1,47 @@
+"""Helpers that read the committed golden fixtures (tests/golden/ir, tests/golden/vectors)."""
+import io
+import json
+import os
+
+import numpy as np
+
+from anvil import irjson
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def ir_path(name):
+    return os.path.join(GOLDEN, "ir", f"{name}.json")
+
+
+def load_ir(name):
+    """(program, raw JSON dict) of a fixture."""
+    with open(ir_path(name)) as f:
+        data = json.load(f)
+    return irjson.load(data), data
+
+
+def vectors(name):
+    return np.load(os.path.join(GOLDEN, "vectors", f"{name}.npz"))
+
+
+def vector_names():
+    d = os.path.join(GOLDEN, "vectors")
+    return sorted(f[:-4] for f in os.listdir(d) if f.endswith(".npz"))
+
+
+def stdout_of(z):
+    return bytes(z["stdout"]).decode()
+
+
+def run_oracle(prog, data, z=None, stdin=""):
+    """Run the oracle on a fixture; function inputs come from the vectors file."""
+    from oracle import interp
+    out = io.StringIO()
+    m = interp.Machine(prog, out=out, seed=data.get("seed", 0), inp=io.StringIO(stdin))
+    if "function" in data and z is not None:
+        by_id = {b.id: b for b in prog.buffers}
+        for k, bid in enumerate(data["function"]["inputs"]):
+            m.arr(by_id[bid])[:] = z[f"input{k}"].reshape(-1)
+    m.run()
+    return m, out.getvalue()

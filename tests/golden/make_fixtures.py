@@ -1,0 +1,110 @@
+"""Write the golden fixtures: kernel IR and interpreter vectors from the reference.
+
+Run in the development container only (the reference checkout is not on the GPU box):
+
+    python tests/golden/make_fixtures.py [/root/reference]
+
+For each program in `programs.py` (Anvil source written for this repository's tests and
+workloads) it writes:
+  - ir/<name>.json       the optimized kernel IR that the reference front end produces
+                          (driver.compile_text: parse -> elaborate -> autodiff -> optimize,
+                          driver.py:33-41), or for a function, pyapi.lower (pyapi.py:114-181);
+  - vectors/<name>.npz    for programs marked `interp`: what the reference interpreter
+                          (interp.py:118-644) prints and the final contents of chosen buffers.
+
+Nothing here is imported by the product, the oracle or the GPU tests; they read the JSON and
+NPZ files. The reference's own code is imported only by this script.
+"""
+from __future__ import annotations
+
+import importlib.util
+import io
+import json
+import os
+import sys
+
+import numpy as np
+
+sys.dont_write_bytecode = True
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+
+
+def _irjson():
+    """This package's serializer, loaded by file path (its dump needs no package import)."""
+    path = os.path.join(REPO, "anvil-lang_amd", "anvil", "irjson.py")
+    spec = importlib.util.spec_from_file_location("_fixture_irjson", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def main(ref_root: str) -> None:
+    sys.path.insert(0, ref_root)
+    from anvil.driver import compile_text          # the reference front end
+    from anvil.interp import Interpreter
+    from anvil import pyapi
+    sys.path.insert(0, HERE)
+    import programs
+
+    irjson = _irjson()
+    os.makedirs(os.path.join(HERE, "ir"), exist_ok=True)
+    os.makedirs(os.path.join(HERE, "vectors"), exist_ok=True)
+    only = set(sys.argv[2:])
+    for spec in programs.PROGRAMS:
+        name = spec["name"]
+        if only and name not in only:
+            continue
+        path = os.path.join(HERE, "programs", f"{name}.anvil")
+        if spec.get("function"):
+            fn = spec["function"]
+            sig = tuple(("tensor", tuple(shape), dtype) for shape, dtype in fn["args"])
+            low = pyapi.lower(spec["source"], path, fn["name"], sig, seed=spec.get("seed", 0))
+            prog = low.prog
+            data = irjson.dump(prog)
+            data["function"] = {"name": fn["name"], "inputs": [b.id for b in low.inputs],
+                                "outputs": [None if b is None else b.id for b in low.outputs]}
+        else:
+            prog = compile_text(spec["source"], path=path, consts=spec.get("consts")).program
+            data = irjson.dump(prog)
+        data["seed"] = spec.get("seed", 0)
+        with open(os.path.join(HERE, "ir", f"{name}.json"), "w") as f:
+            json.dump(data, f, separators=(",", ":"))
+        nk = sum(1 for _ in _kernels(data["main"]))
+        print(f"{name}: {nk} kernels", flush=True)
+        if not spec.get("interp"):
+            continue
+        out = io.StringIO()
+        it = Interpreter(prog, out=out, seed=spec.get("seed", 0), inp=io.StringIO(spec.get("stdin", "")))
+        arrays = {}
+        if spec.get("function"):
+            rng = np.random.default_rng(spec["function"].get("input_seed", 2))
+            for k, (b, (shape, dtype)) in enumerate(zip(low.inputs, spec["function"]["args"])):
+                x = (rng.standard_normal(shape).astype(np.float32) if dtype == "f32"
+                     else rng.integers(0, spec["function"].get("int_hi", 10), shape).astype(np.int32))
+                it.arr(b)[:b.numel] = x.reshape(-1)
+                arrays[f"input{k}"] = x
+        it.run()
+        by_name = {b.name: b for b in prog.buffers}
+        for bname in spec.get("keep", []):
+            b = by_name[bname]
+            arrays[f"buf:{bname}"] = it.arr(b)[:b.numel].reshape(b.shape).copy()
+        if spec.get("function"):
+            for k, b in enumerate(low.outputs):
+                if b is not None:
+                    arrays[f"output{k}"] = it.arr(b)[:b.numel].reshape(b.shape).copy()
+        arrays["stdout"] = np.frombuffer(out.getvalue().encode(), dtype=np.uint8)
+        np.savez_compressed(os.path.join(HERE, "vectors", f"{name}.npz"), **arrays)
+
+
+def _kernels(stmts):
+    for s in stmts:
+        if s["t"] == "kernel":
+            yield s
+        for key in ("body", "then", "else", "cond_block"):
+            if key in s:
+                yield from _kernels(s[key])
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -1,0 +1,452 @@
+"""The Anvil programs behind the golden fixtures (written for this repository).
+
+Each entry: name, source, optional consts (the `--set` overrides), seed, and
+  interp: True    -> the reference interpreter runs it and its vectors are kept,
+  keep: [...]     -> buffer names whose final contents are kept,
+  function: {...} -> lower one function with pyapi.lower for these argument shapes,
+  stdin: "..."    -> what `input` reads.
+The configurations C1-C5 are the workloads named in BASELINE.json; the rest restate the cases of
+the reference's CUDA backend tests (tests/test_cuda.py:26-159) as programs of their own.
+"""
+
+# ----------------------------------------------------------------------------- C1: MLP 784-128-10, SGD
+
+C1 = """
+const N = 60000
+const NT = 10000
+const EPOCHS = 1
+const BATCH = 64
+
+kx: i32[N, 784] ~ randint(0, 256)
+X = f32(kx) / 255
+labels: i32[N] ~ randint(0, 10)
+kt: i32[NT, 784] ~ randint(0, 256)
+X_test = f32(kt) / 255
+test_labels: i32[NT] ~ randint(0, 10)
+
+model MLP:
+    l1 = Linear(784, 128)
+    l2 = Linear(128, 10)
+    fn forward(x: [n, 784]) -> [n, 10] = x |> l1 |> relu |> l2
+
+net = MLP()
+
+for epoch in range(EPOCHS):
+    for x, y in batches(X, labels, size=BATCH, shuffle=true):
+        loss = cross_entropy(net(x), y)
+        minimize loss with sgd(lr=0.1)
+    acc = accuracy(net(X_test), test_labels)
+    print("epoch {epoch + 1}   loss {loss:.4f}   test accuracy {acc:.4f}")
+"""
+
+# ----------------------------------------------------------------------------- C2: MLP 784-1024-1024-10, Adam
+
+C2 = """
+const N = 65536
+const H = 1024
+const BATCH = 256
+const STEPS = 500
+const EPOCHS = 2
+
+X: [N, 784] ~ uniform(0, 1)
+labels: i32[N] ~ randint(0, 10)
+
+seed(1)
+model WideMLP:
+    l1 = Linear(784, H)
+    l2 = Linear(H, H)
+    l3 = Linear(H, 10)
+    fn forward(x) = x |> l1 |> relu |> l2 |> relu |> l3
+
+net = WideMLP()
+
+step = 0
+for epoch in range(EPOCHS):
+    for x, y in batches(X, labels, size=BATCH, shuffle=true):
+        if step >= STEPS:
+            break
+        loss = cross_entropy(net(x), y)
+        minimize loss with adam(lr=1e-3)
+        step += 1
+print("steps {step}   loss {loss:.4f}")
+"""
+
+# ----------------------------------------------------------------------------- C3: standalone functions
+
+C3_SOFTMAX = """
+fn rows_softmax(x: [n, d]) = softmax(x)
+"""
+
+C3_LAYERNORM = """
+fn norm(x: [n, d], g: [d], b: [d]) = layer_norm(x) * g + b
+"""
+
+C3_LINEAR = """
+fn linear(x: [n, k], W: [o, k], b: [o]):
+    y[i, j] = sum W[j, c] * x[i, c] + b[j]
+    return y
+"""
+
+C3_ATTENTION = """
+fn attention(q: [b, t, d], k: [b, t, d], v: [b, t, d]):
+    s[n, i, j] = sum q[n, i, c] * k[n, j, c] / sqrt(d)
+    return softmax(s) @ v
+"""
+
+# ----------------------------------------------------------------------------- C4: char transformer
+
+C4 = """
+const STEPS = 200
+const BATCH = 16
+const T = 64
+const D = 256
+const HEADS = 4
+const DH = D // HEADS
+const V = 96
+const LAYERS = 4
+
+seed(3)
+
+model Block:
+    param Wq: [D, D] ~ normal(0, sqrt(1 / D))
+    param Wk: [D, D] ~ normal(0, sqrt(1 / D))
+    param Wv: [D, D] ~ normal(0, sqrt(1 / D))
+    param Wo: [D, D] ~ normal(0, sqrt(0.5 / D))
+    up = Linear(D, 4 * D)
+    down = Linear(4 * D, D)
+    fn forward(x):
+        h = layer_norm(x)
+        q = (h @ Wq).reshape(-1, T, HEADS, DH)
+        k = (h @ Wk).reshape(-1, T, HEADS, DH)
+        v = (h @ Wv).reshape(-1, T, HEADS, DH)
+        s[b, a, i, j] = sum q[b, i, a, e] * k[b, j, a, e] / sqrt(DH) + (0.0 if j <= i else -1e9)
+        p = softmax(s)
+        o[b, i, a, e] = sum p[b, a, i, j] * v[b, j, a, e]
+        x = x + o.reshape(-1, T, D) @ Wo
+        return x + (layer_norm(x) |> up |> gelu |> down)
+
+model GPT:
+    param E: [V, D] ~ normal(0, 0.5)
+    param P: [T, D] ~ normal(0, 0.1)
+    blocks = [Block() for n in range(LAYERS)]
+    out = Linear(D, V)
+    fn forward(codes):
+        e[b, t, d] = E[codes[b, t], d] + P[t, d]
+        static for blk in blocks:
+            e = blk(e)
+        return e |> layer_norm |> out
+
+net = GPT()
+
+for step in range(STEPS):
+    x: i32[BATCH, T + 1] ~ randint(0, V)
+    logits = net(x[:, 0:T])
+    loss = cross_entropy(logits.reshape(BATCH * T, V), x[:, 1:T + 1].reshape(BATCH * T))
+    minimize loss over net with adam(lr=1e-3)
+print("loss {loss:.4f}")
+"""
+
+# ----------------------------------------------------------------------------- C5: small CNN
+
+C5 = """
+const STEPS = 300
+const NB = 128
+const C1 = 32
+const C2 = 64
+const HID = 128
+
+seed(4)
+X: [NB, 1, 28, 28] ~ uniform(0, 1)
+Y: i32[NB] ~ randint(0, 10)
+
+model Net:
+    c1 = Conv2d(1, C1, 3)
+    c2 = Conv2d(C1, C2, 3)
+    fc1 = Linear(C2 * 12 * 12, HID)
+    fc2 = Linear(HID, 10)
+    fn forward(x) = x |> c1 |> relu |> c2 |> relu |> max_pool2d |> flatten(1) |> fc1 |> relu |> fc2
+
+net = Net()
+
+for step in range(STEPS):
+    loss = cross_entropy(net(X), Y)
+    minimize loss with sgd(lr=0.05)
+print("loss {loss:.4f}")
+"""
+
+# ----------------------------------------------------------------------------- test programs
+
+HELLO = """
+x = [1.0, 2.0, 3.0]
+W = [[1.0, 0.0, -1.0],
+     [0.5, 0.5,  0.5]]
+y[i] = sum W[i, j] * x[j]
+print("y = {y}")
+outer[i, j] = x[i] * x[j]
+print(outer)
+print("softmax {softmax(x)} max {max(x)} mean {mean(x):.3f}")
+noise: [2, 3] ~ normal(0, 1)
+print("noise = {noise}")
+param w: [3]
+loss = sum((w - x) ** 2)
+dw = grad(loss, w)
+print("dw {dw}")
+"""
+
+LINREG = """
+n = 1000
+X: [n, 3] ~ normal(0, 1)
+noise: [n] ~ normal(0, 0.1)
+y = X @ [2.0, -3.4, 1.7] + 4.2 + noise
+
+param w: [3]
+param b: f32
+
+for step in range(100):
+    loss = mse(X @ w + b, y)
+    minimize loss with sgd(lr=0.1)
+    if step % 20 == 0:
+        print("step {step:3d}   loss {loss:.5f}")
+
+print("learned w = {w}   b = {b:.3f}")
+"""
+
+ATTENTION_TRAIN = """
+B = 8
+T = 16
+d = 24
+h = 8
+
+fn attention(x: [b, t, dm], Wq: [dm, dh], Wk: [dm, dh], Wv: [dm, dh]) -> [b, t, dh]:
+    q = x @ Wq
+    k = x @ Wk
+    v = x @ Wv
+    s[..., i, j] = sum q[..., i, c] * k[..., j, c] / sqrt(dh)
+    p = softmax(s)
+    out[..., i, c] = sum p[..., i, j] * v[..., j, c]
+    return out
+
+Tq: [d, h] ~ normal(0, 0.4)
+Tk: [d, h] ~ normal(0, 0.4)
+Tv: [d, h] ~ normal(0, 0.4)
+
+param Wq: [d, h] ~ normal(0, 0.2)
+param Wk: [d, h] ~ normal(0, 0.2)
+param Wv: [d, h] ~ normal(0, 0.2)
+
+for step in range(1, 61):
+    x: [B, T, d] ~ normal(0, 1)
+    loss = mse(attention(x, Wq, Wk, Wv), attention(x, Tq, Tk, Tv))
+    minimize loss with adam(lr=0.01)
+    if step % 20 == 0:
+        print("step {step:3d}   loss {loss:.5f}")
+"""
+
+SPLIT = """
+x: [300000] ~ normal(0, 1)
+print("sum {sum(x):.2f}  max {max(x):.4f}  min {min(x):.4f}  mean {mean(x):.5f}")
+W: [3, 50000] ~ uniform(-1, 1)
+y: [50000] ~ normal(0, 1)
+v[i] = sum W[i, j] * y[j]
+print(v)
+print(argmax(x))
+print(argmin(x))
+R = rand(3, 50000)
+noisy[i] = sum W[i, j] * R[i, j]
+print(noisy)
+"""
+
+SCATTER = """
+labels: i32[1000] ~ randint(0, 10)
+counts: i32[10] = 0
+counts[labels[i]] += 1
+print(counts)
+E: [10, 4] ~ normal(0, 1)
+rows[i, d] = E[labels[i], d]
+print(rows[0:5])
+hist: [10] = 0.0
+hist[labels[i]] += 0.5
+print(hist)
+"""
+
+BOUNDS = """
+x = arange(10)
+for i in range(12):
+    s = x[i]
+    print(s)
+"""
+
+GATHER_OOB = """
+idx: i32[4] = [0, 1, 7, 2]
+E: [5, 3] ~ normal(0, 1)
+r[i, d] = E[idx[i], d]
+print(r)
+"""
+
+ASSERT_FAIL = """
+x = sum(rand(3)) + 3
+assert x < 2, "x is too big"
+print("unreachable")
+"""
+
+SAVE_LOAD = """
+param W: [3, 4] ~ normal(0, 1)
+loaded = load(W, "CKPT")
+if loaded == 0:
+    save(W, "CKPT")
+print("loaded {loaded} sum {sum(W):.4f}")
+"""
+
+INTEGERS = """
+a: i32[12] = [-7, -6, -5, -1, 0, 1, 5, 6, 7, 2147483647, -2147483647, 13]
+b: i32[12] = [2, -4, 3, 5, 3, -2, 0, 4, -3, 1, 2, -5]
+print(a // b)
+print(a % b)
+print(a + b)
+print(a * b)
+fa = f32(a) / 4
+print(fa // 1.5)
+print(fa % -1.5)
+print(i32(fa))
+print(round(fa))
+print(floor(fa))
+print(ceil(fa))
+print(sign(fa))
+print(abs(a))
+print(max(fa, 0.5))
+print(min(a, 3))
+v = [1.5, -2.25, 0.0, 3.75]
+print(exp(v))
+print(log(abs(v) + 1))
+print(sqrt(abs(v)))
+print(tanh(v))
+print(sigmoid(v))
+print(sin(v))
+print(cos(v))
+print(v ** 2)
+print(f32(v > 0) + f32(v <= 0) * 2)
+print(argmax(v))
+print(prod(v + 3))
+"""
+
+FORMATS = """
+big: [40, 30] ~ normal(0, 1000)
+print(big)
+small: [3, 4] ~ uniform(0, 0.0001)
+print(small)
+i3: i32[2, 3, 4] ~ randint(-50, 50)
+print(i3)
+long: i32[2000] ~ randint(0, 100)
+print(long)
+z = 0.0
+print("zero {z} int {i3[1, 2, 3]} f {z:.2f}")
+"""
+
+CONTROL = """
+total = 0
+k = 0
+while k < 10:
+    k += 1
+    if k % 3 == 0:
+        continue
+    total += k
+    if total > 20:
+        break
+print("k {k} total {total}")
+acc = 0.0
+for i in range(5):
+    for j in range(i, 5):
+        acc += f32(i * j)
+print("acc {acc}")
+"""
+
+PRODUCTS = """
+x: [6, 40] ~ uniform(0.9, 1.1)
+p[i] = prod x[i, j]
+print(p)
+mx[i] = max x[i, j]
+mn[i] = min x[i, k]
+print(mx - mn)
+a[i] = argmax x[i, j]
+print(a)
+"""
+
+MNIST_LIKE = """
+const N = 2048
+const NT = 512
+const EPOCHS = 2
+
+kx: i32[N, 784] ~ randint(0, 256)
+X = f32(kx) / 255
+labels: i32[N] ~ randint(0, 10)
+kt: i32[NT, 784] ~ randint(0, 256)
+X_test = f32(kt) / 255
+test_labels: i32[NT] ~ randint(0, 10)
+
+model MLP:
+    l1 = Linear(784, 128)
+    l2 = Linear(128, 10)
+    fn forward(x: [n, 784]) -> [n, 10] = x |> l1 |> relu |> l2
+
+net = MLP()
+
+for epoch in range(EPOCHS):
+    for x, y in batches(X, labels, size=64, shuffle=true):
+        loss = cross_entropy(net(x), y)
+        minimize loss with sgd(lr=0.1)
+    acc = accuracy(net(X_test), test_labels)
+    print("epoch {epoch + 1}   loss {loss:.4f}   test accuracy {acc:.4f}")
+"""
+
+C1_KEEP = ["net.l1.W", "net.l1.b", "net.l2.W", "net.l2.b", "perm"]
+C2_KEEP = ["net.l1.W", "net.l1.b", "net.l2.W", "net.l2.b", "net.l3.W", "net.l3.b", "perm"]
+
+PROGRAMS = [
+    # the workloads at the sizes BASELINE.json names (IR only: the interpreter would take hours)
+    {"name": "c1_mlp", "source": C1},
+    {"name": "c2_wide_mlp", "source": C2},
+    {"name": "c4_transformer", "source": C4},
+    {"name": "c4_transformer_t256", "source": C4, "consts": {"T": 256}},
+    {"name": "c5_cnn", "source": C5},
+    {"name": "c3_softmax", "source": C3_SOFTMAX,
+     "function": {"name": "rows_softmax", "args": [([8192, 4096], "f32")]}},
+    {"name": "c3_layernorm", "source": C3_LAYERNORM,
+     "function": {"name": "norm", "args": [([8192, 1024], "f32"), ([1024], "f32"), ([1024], "f32")]}},
+    {"name": "c3_linear", "source": C3_LINEAR,
+     "function": {"name": "linear", "args": [([8192, 4096], "f32"), ([4096, 4096], "f32"), ([4096], "f32")]}},
+    {"name": "c3_attention", "source": C3_ATTENTION,
+     "function": {"name": "attention", "args": [([4, 2048, 128], "f32")] * 3}},
+    # the same workloads at sizes the interpreter finishes in seconds (IR + vectors)
+    {"name": "c1_small", "source": C1, "consts": {"N": 640, "NT": 256}, "interp": True, "keep": C1_KEEP},
+    {"name": "c2_small", "source": C2, "consts": {"N": 1024, "H": 96, "BATCH": 32, "STEPS": 40},
+     "interp": True, "keep": C2_KEEP},
+    {"name": "c2_steps100", "source": C2, "consts": {"N": 2048, "H": 64, "BATCH": 32, "STEPS": 100},
+     "interp": True, "keep": C2_KEEP},
+    {"name": "c4_small", "source": C4,
+     "consts": {"STEPS": 3, "BATCH": 2, "T": 8, "D": 32, "HEADS": 2, "LAYERS": 2}, "interp": True},
+    {"name": "c5_small", "source": C5, "consts": {"STEPS": 3, "NB": 4, "C1": 4, "C2": 8, "HID": 16},
+     "interp": True},
+    {"name": "c3_softmax_small", "source": C3_SOFTMAX, "interp": True,
+     "function": {"name": "rows_softmax", "args": [([64, 300], "f32")]}},
+    {"name": "c3_layernorm_small", "source": C3_LAYERNORM, "interp": True,
+     "function": {"name": "norm", "args": [([48, 200], "f32"), ([200], "f32"), ([200], "f32")]}},
+    {"name": "c3_linear_small", "source": C3_LINEAR, "interp": True,
+     "function": {"name": "linear", "args": [([96, 80], "f32"), ([72, 80], "f32"), ([72], "f32")]}},
+    {"name": "c3_attention_small", "source": C3_ATTENTION, "interp": True,
+     "function": {"name": "attention", "args": [([2, 64, 32], "f32")] * 3}},
+    # the reference's CUDA backend test cases as programs
+    {"name": "hello", "source": HELLO, "interp": True},
+    {"name": "linreg", "source": LINREG, "interp": True, "keep": ["w", "b"]},
+    {"name": "attention_train", "source": ATTENTION_TRAIN, "interp": True},
+    {"name": "split", "source": SPLIT, "interp": True},
+    {"name": "scatter", "source": SCATTER, "interp": True},
+    {"name": "bounds", "source": BOUNDS},
+    {"name": "gather_oob", "source": GATHER_OOB},
+    {"name": "assert_fail", "source": ASSERT_FAIL},
+    {"name": "save_load", "source": SAVE_LOAD},
+    {"name": "integers", "source": INTEGERS, "interp": True},
+    {"name": "formats", "source": FORMATS, "interp": True},
+    {"name": "control", "source": CONTROL, "interp": True},
+    {"name": "products", "source": PRODUCTS, "interp": True},
+    {"name": "mnist_like", "source": MNIST_LIKE, "interp": True, "keep": C1_KEEP},
+]
