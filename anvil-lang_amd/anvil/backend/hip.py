@@ -1,0 +1,748 @@
+"""The MI355X backend: Anvil's kernel IR as one .hip file, compiled into a gfx950 shared library.
+
+This is the HIP counterpart of the reference's CUDA backend (anvil/backend/cuda.py:636-663), with
+the same plugin interface:
+
+    generate(prog, seed=0, library=False) -> str        the whole .hip source
+    build(source, lib_path)                              hipcc --offload-arch=gfx950 ... -shared
+    load(prog, seed=0, library=False) -> HipLibrary      generate + build (cached) + ctypes
+
+and a C ABI that the reference's library mode defines (aarch64.py:141-142, 162-167; pyapi.py:
+266-296): `int anvil_entry(void)` and the `anvil_input<k>` / `anvil_output<k>` pointer slots, plus
+`int anvil_main(void)` for a whole program (what `anvil run` executes).
+
+How the program runs on the GPU:
+  - every device buffer lives in one hipMalloc'ed arena, at offsets from a lifetime plan in which
+    temporaries that are never live together share bytes (hip_analysis.plan_arena);
+  - each IR kernel, or a run of kernels over the same rows, becomes one HIP kernel with a schedule
+    chosen for its shape (hip_kernels: map, serial, rows, split; hip_gemm: fp32 MFMA products with
+    the kernel's own statements as the epilogue);
+  - loop counters and the scalars computed only from them stay on the host and reach kernels as
+    arguments (hip_analysis.host_scalars), so a training loop enqueues work without waiting;
+  - the host waits for the device only where it needs a device value (a print, an `if` on a device
+    scalar, a data file, a checkpoint) and then reports the first bounds fault a kernel latched.
+
+Generation is deterministic: the same program gives the same bytes, so built libraries are cached
+by the hash of their source.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import os
+import shutil
+import subprocess
+import tempfile
+import threading
+
+from .. import ir
+from ..ir import F32, I32, Buffer, KernelStmt
+from . import hip_analysis as A
+from . import hip_cost
+from . import hip_kernels as HK
+from .hip_emit import Emitter, Scope, c_string, ctype, flit, ilit, sanitize
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+RUNTIME_DIR = os.path.join(HERE, "hip_rt")
+ARCH = "gfx950"
+
+
+class HipToolchainError(Exception):
+    pass
+
+
+def runtime_source() -> str:
+    """anvil_rt.h and anvil_hip.h (and the MFMA templates), inlined: a generated file stands alone."""
+    def read(name):
+        with open(os.path.join(RUNTIME_DIR, name)) as f:
+            return f.read().replace("#pragma once\n", "")
+    rt = read("anvil_rt.h")
+    dev = read("anvil_hip.h").replace('#include "anvil_rt.h"', rt)
+    gemm_path = os.path.join(RUNTIME_DIR, "anvil_mfma.h")
+    if os.path.exists(gemm_path):
+        dev += "\n" + read("anvil_mfma.h")
+    return dev
+
+
+# ----------------------------------------------------------------------------- host-side scope
+
+class HostScope(Scope):
+    """A scalar kernel computed on the host from host scalars and constants."""
+
+    device = False
+
+    def __init__(self, gen):
+        self.gen = gen
+
+    def var(self, v):
+        raise AssertionError("a host kernel has no loop variables")
+
+    def buf(self, b):
+        r = b.root
+        if r.kind == "const" and r.init is not None:
+            return f"anvil_init{r.id}"
+        raise AssertionError(f"host kernel reads device buffer {r.name}")
+
+    def host_scalar(self, b):
+        if b.root.id in self.gen.hosts:
+            return f"anvil_h{b.root.id}"
+        return None
+
+    def rand_index(self):
+        return "0"
+
+    def stream(self):
+        return "0u"
+
+    def seed(self):
+        return "anvil_hs.seed"
+
+    def fault(self, message):
+        return self.gen.fault(message)
+
+
+# ----------------------------------------------------------------------------- the generator
+
+class HipGen:
+    def __init__(self, prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False):
+        self.prog = prog
+        self.seed = seed & 0xFFFFFFFF
+        self.library = library
+        self.emulate = emulate
+        self.hosts = A.host_scalars(prog)
+        self.readers = A.all_readers(prog)
+        self.by_id = {b.root.id: b.root for b in prog.buffers}
+        self.faults: list[str] = []
+        self.tables: list[str] = []
+        self.plans: list = []
+        self.plan_of: dict = {}           # first kernel id -> plan (a run of kernels shares one)
+        self.group_of: dict = {}          # kernel id -> the plan it is a stage of
+        self.device_bufs: dict[int, Buffer] = {}
+        self.mirrored: dict[int, Buffer] = {}
+        self.ckpts: list[str] = []
+        self.n_labels = 0
+        self.gemm = None
+        if not emulate:
+            try:
+                from . import hip_gemm
+                self.gemm = hip_gemm
+            except ImportError:
+                self.gemm = None
+
+    # ------------------------------------------------------------------ small helpers
+    def fault(self, message: str) -> int:
+        if message in self.faults:
+            return self.faults.index(message) + 1
+        if len(self.faults) >= 254:
+            message = "index out of bounds"
+            if message in self.faults:
+                return self.faults.index(message) + 1
+        self.faults.append(message)
+        return len(self.faults)
+
+    def label(self, hint: str) -> str:
+        self.n_labels += 1
+        return f"{hint}{self.n_labels}"
+
+    def table(self, ctype_: str, items) -> str:
+        name = self.label("anvil_tab")
+        self.tables.append(f"static const {ctype_} {name}[] = {{{', '.join(items) or '0'}}};")
+        return name
+
+    def strings(self, strs) -> str:
+        return self.table("char *const", [c_string(s) for s in strs])
+
+    def is_host(self, b) -> bool:
+        return b.root.id in self.hosts
+
+    def dev(self, b) -> str:
+        """Host code: the device pointer of a buffer."""
+        r = b.root
+        self.device_bufs.setdefault(r.id, r)
+        return f"anvil_b{r.id}"
+
+    def mirror(self, b) -> str:
+        r = b.root
+        self.dev(r)
+        self.mirrored.setdefault(r.id, r)
+        return f"anvil_mir{r.id}"
+
+    def host_view(self, b) -> str:
+        """Host code: a host pointer holding b's current contents (fetching it if needed)."""
+        r = b.root
+        if self.is_host(r):
+            return f"(&anvil_h{r.id})"
+        return f"(({ctype(r.dtype)} *)anvil_fetch(&{self.mirror(r)}))"
+
+    def scalar_value(self, b) -> str:
+        r = b.root
+        if self.is_host(r):
+            return f"anvil_h{r.id}"
+        return f"anvil_read_{'i32' if r.dtype == I32 else 'f32'}({self.dev(r)})"
+
+    # ------------------------------------------------------------------ planning kernels
+    def plan_run(self, stmts: list, i: int):
+        """The plan for the kernel at stmts[i] and how many statements it takes."""
+        k = stmts[i].kernel
+        name = f"k{k.id}"
+        parallel = A.parallel_safe(k)
+        if not parallel:
+            return HK.SerialPlan(self, k, name), 1
+        if k.red is None:
+            return HK.MapPlan(self, k, name), 1
+        if self.gemm is not None:
+            g = self.gemm.match(self, k, name)
+            if g is not None:
+                return g, 1
+        ty = HK.split_ways(k, self.emulate)
+        if ty > 1:
+            return HK.SplitPlan(self, k, name, ty), 1
+        if k.red.op in ("argmax", "argmin") or any(st.accumulate for st in k.stores):
+            return HK.RowsPlan(self, [k], name, HK.rows_lanes(k, self.emulate), self.emulate), 1
+        gb = HK.GroupBuilder(k)
+        j = i + 1
+        while j < len(stmts) and isinstance(stmts[j], KernelStmt) and gb.fits(stmts[j].kernel, self.hosts):
+            gb.add(stmts[j].kernel)
+            j += 1
+        plan = HK.RowsPlan(self, gb.kernels, name, HK.rows_lanes(k, self.emulate), self.emulate)
+        self.mark_dead_stores(plan)
+        return plan, j - i
+
+    def mark_dead_stores(self, plan):
+        """Stores of a row group whose buffer only the group reads (from registers) are dropped."""
+        if len(plan.kernels) < 2:
+            return
+        readers_in: dict[int, int] = {}
+        for k in plan.kernels:
+            for b in A.kernel_reads(k):
+                readers_in[b.id] = readers_in.get(b.id, 0) + 1
+        for k in plan.kernels:
+            cm = plan.canon_map(k)
+            _, inner = plan.stage_vars(k)
+            for i, st in enumerate(k.stmts):
+                if not isinstance(st, ir.Store):
+                    continue
+                b = st.buf.root
+                if b.kind not in A.SHARED_KINDS or self.is_host(b) or getattr(b, "heap", False):
+                    continue
+                if self.readers.get(b.id, 0) != readers_in.get(b.id, 0):
+                    continue
+                key = HK.canon_key(st.buf, st.offset, cm)
+                element = k.red is None and bool(inner)
+                if key is None or (element and key not in plan.cache_arrays):
+                    continue
+                plan.skip_stores.add((k.id, i))
+
+    # ------------------------------------------------------------------ host code
+    def block(self, blk: ir.Block, ind: str) -> list[str]:
+        out = []
+        stmts = blk.stmts
+        i = 0
+        while i < len(stmts):
+            st = stmts[i]
+            if isinstance(st, KernelStmt):
+                k = st.kernel
+                if A.is_host_kernel(k, self.hosts):
+                    out += self.host_kernel(k, ind)
+                    i += 1
+                    continue
+                plan = self.plan_of.get(k.id)
+                if plan is None:
+                    plan, used = self.plan_run(stmts, i)
+                    self.plans.append(plan)
+                    self.plan_of[k.id] = (plan, used)
+                    for kk in plan.kernels:
+                        self.group_of[kk.id] = plan
+                else:
+                    plan, used = plan
+                out += self.launch(plan, ind)
+                i += used
+                continue
+            out += self.stmt(st, ind)
+            i += 1
+        return out
+
+    def host_kernel(self, k: ir.Kernel, ind: str) -> list[str]:
+        lines = [f"{ind}{{   // {k.name}: on the host"]
+        em = Emitter(HostScope(self), lines, ind + "    ")
+        for st in k.stmts:
+            if isinstance(st, ir.Let):
+                em.let(st)
+                continue
+            val = em.store_value(st)
+            em.emit(f"anvil_h{st.buf.root.id} = {val};")
+            em.reset_memo()
+        lines.append(f"{ind}}}")
+        return lines
+
+    def launch(self, plan, ind: str) -> list[str]:
+        out = [f"{ind}{{   // {plan.label}"]
+        streams = []
+        for n, _ in enumerate(plan.streams):
+            out.append(f"{ind}    const uint32_t s{n} = anvil_hs.stream++;")
+            streams.append(f"s{n}")
+        if not hasattr(plan, "_source"):
+            plan._source = plan.source()
+        site = self.plans.index(plan)
+        blocks, threads = plan.grid()
+        args = plan.launch_args(streams)
+        for b in plan.bufs.values():
+            self.dev(b)
+        go = "ANVIL_GO3" if isinstance(blocks, tuple) else "ANVIL_GO"
+        grid = ", ".join(str(x) for x in blocks) if isinstance(blocks, tuple) else str(blocks)
+        out.append(f"{ind}    anvil_prof_enter({site});")
+        out.append(f"{ind}    {go}({plan.name}, {grid}, {threads}, {', '.join(args)});")
+        out.append(f"{ind}    anvil_prof_leave();")
+        for b in sorted(plan.writes(), key=lambda b: b.id):
+            out.append(f"@@dirty {b.id} {ind}    ")
+        out.append(f"{ind}}}")
+        return out
+
+    def stmt(self, st, ind: str) -> list[str]:
+        if isinstance(st, ir.For):
+            return self.for_(st, ind)
+        if isinstance(st, ir.While):
+            out = [f"{ind}while (1) {{"] + self.block(st.cond_block, ind + "    ")
+            out.append(f"{ind}    if ({self.scalar_value(st.cond)} == 0) break;")
+            return out + self.block(st.body, ind + "    ") + [f"{ind}}}"]
+        if isinstance(st, ir.If):
+            out = [f"{ind}if ({self.scalar_value(st.cond)} != 0) {{"] + self.block(st.then, ind + "    ")
+            if st.orelse.stmts:
+                out += [f"{ind}}} else {{"] + self.block(st.orelse, ind + "    ")
+            return out + [f"{ind}}}"]
+        if isinstance(st, ir.Break):
+            return [f"{ind}break;"]
+        if isinstance(st, ir.Continue):
+            return [f"{ind}continue;"]
+        if isinstance(st, ir.Print):
+            return self.print_(st, ind)
+        if isinstance(st, ir.Check):
+            loc = f"{st.span.location()}: " if st.span is not None and st.span.location() else ""
+            terms = [f"{c}LL * (long long){self.scalar_value(t.buf)}" for t, c in st.value.terms.items()
+                     if isinstance(t, ir.ScalarRef)]
+            v = " + ".join([f"{st.value.const}LL"] + terms)
+            return [f"{ind}{{ const long long v_ = {v};",
+                    f"{ind}  if (v_ < {st.lo}LL || v_ > {st.hi}LL) {{ anvil_sync(); "
+                    f"anvil_bad_value({c_string(loc + st.message)}, v_); }} }}"]
+        if isinstance(st, ir.RTCall):
+            return [ind + line for line in self.rtcall(st)]
+        raise NotImplementedError(type(st).__name__)
+
+    def for_(self, st: ir.For, ind: str) -> list[str]:
+        c = st.counter.root
+        start = str(st.start) if isinstance(st.start, int) else f"(long long){self.scalar_value(st.start)}"
+        stop = str(st.stop) if isinstance(st.stop, int) else f"(long long){self.scalar_value(st.stop)}"
+        name = c_string(c.name)
+        out = [f"{ind}{{", f"{ind}    const long long stop_ = {stop};"]
+        if self.is_host(c):
+            out.append(f"{ind}    for (anvil_h{c.id} = (int)({start}); anvil_h{c.id} < stop_; anvil_h{c.id} += {st.step}) {{")
+            out.append(f"{ind}        anvil_mark({name});")
+            out += self.block(st.body, ind + "        ")
+            out.append(f"{ind}    }}")
+        else:
+            d = self.dev(c)
+            out.append(f"{ind}    for (long long c_ = {start}; c_ < stop_; c_ = (long long)anvil_read_i32({d}) + {st.step}) {{")
+            out.append(f"{ind}        anvil_write_i32({d}, (int)c_);")
+            out.append(f"@@dirty {c.id} {ind}        ")
+            out.append(f"{ind}        anvil_mark({name});")
+            out += self.block(st.body, ind + "        ")
+            out.append(f"{ind}    }}")
+        out.append(f"{ind}}}")
+        return out
+
+    def print_(self, st: ir.Print, ind: str) -> list[str]:
+        f = "stderr" if st.err else "stdout"
+        out = [f"{ind}anvil_sync();"]
+        if st.err:
+            out.append(f"{ind}fflush(stdout);")
+        for it in list(st.items) + [ir.PrintItem("text", st.end)]:
+            if it.kind == "text":
+                if it.text:
+                    out.append(f"{ind}fputs({c_string(it.text)}, {f});")
+            elif it.kind == "scalar":
+                b = it.buf.root
+                v = f"{self.host_view(b)}[0]"
+                if it.fmt:
+                    isint = b.dtype == I32 or it.fmt.endswith("d")
+                    val = (f"(int){v}" if b.dtype == I32 else f"(int){v}") if isint else f"(double){v}"
+                    out.append(f"{ind}fprintf({f}, {c_string(it.fmt)}, {val});")
+                elif b.dtype == I32:
+                    out.append(f"{ind}fprintf({f}, \"%d\", {v});")
+                else:
+                    out.append(f"{ind}anvil_put_f32({f}, {v});")
+            elif it.kind == "tensor":
+                b = it.buf.root
+                dims = self.table("long", [str(d) for d in b.shape])
+                out.append(f"{ind}anvil_put_tensor({self.host_view(b)}, {1 if b.dtype == I32 else 0}, {len(b.shape)}, {dims});")
+            elif it.kind == "pick":
+                tab = self.strings(it.choices)
+                out.append(f"{ind}anvil_put_choice({f}, (int){self.host_view(it.buf)}[0], {tab}, {len(it.choices)});")
+            elif it.kind == "chars":
+                out.append(f"{ind}anvil_put_chars((const int *){self.host_view(it.buf)}, {it.buf.numel});")
+            else:
+                raise NotImplementedError(it.kind)
+        return out
+
+    def writable(self, b, full: bool) -> str:
+        """Host code: prepare b's mirror for a host write (the caller commits it afterwards)."""
+        return f"(({ctype(b.root.dtype)} *)anvil_begin_write(&{self.mirror(b)}, {1 if full else 0}))"
+
+    def rtcall(self, st: ir.RTCall) -> list[str]:
+        a, n = st.args, st.name
+        b = a.get("buf")
+        if n == "seed":
+            return [f"anvil_hs.seed = {a['value'] & 0xFFFFFFFF}u; anvil_hs.stream = 0;"]
+        if n == "skip_rand":
+            return ["anvil_hs.stream++;"]
+        if n == "exit":
+            return ["anvil_sync();", "fflush(stdout);", f"exit({int(a['value'])});"]
+        if n in ("iota", "iota_once"):
+            return [f"anvil_fill_iota((int *){self.writable(b, True)}, {b.numel}L); anvil_commit(&{self.mirror(b)});"]
+        if n == "shuffle":
+            if self.is_host(b):
+                return [f"anvil_fisher_yates(&anvil_h{b.root.id}, {b.numel}L);"]
+            return [f"anvil_fisher_yates((int *){self.writable(b, False)}, {b.numel}L); anvil_commit(&{self.mirror(b)});"]
+        if n == "clock":
+            return ["anvil_sync();", f"{self.writable(b, True)}[0] = (float)(anvil_seconds() - anvil_hs.t0); "
+                    f"anvil_commit(&{self.mirror(b)});"]
+        if n == "sleep":
+            return ["anvil_sync();", "fflush(stdout);",
+                    f"{{ const float s_ = {self.host_view(b)}[0]; if (s_ > 0) usleep((useconds_t)(s_ * 1e6f)); }}"]
+        if n == "nonzero":
+            src = a["src"]
+            return [f"anvil_find_nonzero((const int *){self.host_view(src)}, {src.numel}L, (int *){self.writable(b, True)}, "
+                    f"{b.numel}L); anvil_commit(&{self.mirror(b)});"]
+        if n == "load_idx":
+            return ["anvil_sync();", f"anvil_read_idx({c_string(a['path'])}, {self.writable(b, True)}, {b.numel}L, "
+                    f"{a['header']}L, {1 if b.dtype == I32 else 0}); anvil_commit(&{self.mirror(b)});"]
+        if n == "load_csv":
+            return ["anvil_sync();", f"anvil_read_csv({c_string(a['path'])}, (float *){self.writable(b, True)}, "
+                    f"{b.numel}L, {a['skip']}L); anvil_commit(&{self.mirror(b)});"]
+        if n == "load_bytes":
+            return ["anvil_sync();", f"anvil_read_bytes({c_string(a['path'])}, (int *){self.writable(b, True)}, "
+                    f"{b.numel}L); anvil_commit(&{self.mirror(b)});"]
+        if n == "load_npy":
+            return ["anvil_sync();", f"anvil_read_npy({c_string(a['path'])}, {self.writable(b, True)}, {b.numel}L, "
+                    f"{a['offset']}L, {a['kind']}, {a['size']}); anvil_commit(&{self.mirror(b)});"]
+        if n == "save_npy":
+            tab = self.table("unsigned char", [str(x) for x in a["header"]])
+            return ["anvil_sync();", f"anvil_write_npy({c_string(a['path'])}, {tab}, {len(a['header'])}L, "
+                    f"{self.host_view(b)}, {4 * b.numel}L);"]
+        if n == "input":
+            return ["anvil_sync();", f"if (anvil_read_number((float *){self.writable(b, True)})) goto anvil_end;",
+                    f"anvil_commit(&{self.mirror(b)});"]
+        if n == "show":
+            return ["anvil_sync();", f"anvil_show_grid((const int *){self.host_view(b)}, {a['rows']}L, {a['cols']}L, "
+                    f"{self.strings(a['glyphs'])}, {len(a['glyphs'])});"]
+        if n in ("save", "load"):
+            tab = self.label("anvil_ckpt")
+            bufs = a["bufs"]
+            self.ckpts.append((tab, bufs))
+            out = ["anvil_sync();"]
+            if n == "save":
+                out.append(f"{{ anvil_ckpt_entry e_[] = {{{', '.join(f'{{(void *){self.host_view(x)}, {ir.ckpt_key(x.root)}ULL}}' for x in bufs)}}};")
+                out.append(f"  anvil_ckpt_save({c_string(a['path'])}, e_, {len(bufs)}L); }}")
+                return out
+            out.append(f"{{ anvil_ckpt_entry e_[] = {{{', '.join(f'{{(void *){self.writable(x, False)}, {ir.ckpt_key(x.root)}ULL}}' for x in bufs)}}};")
+            out.append(f"  const float ok_ = anvil_ckpt_load({c_string(a['path'])}, e_, {len(bufs)}L);")
+            for x in bufs:
+                out.append(f"  anvil_commit(&{self.mirror(x)});")
+            if self.is_host(b):
+                out.append(f"  anvil_h{b.root.id} = ok_; }}")
+            else:
+                out.append(f"  {self.writable(b, True)}[0] = ok_; anvil_commit(&{self.mirror(b)}); }}")
+            return out
+        raise NotImplementedError(n)
+
+    # ------------------------------------------------------------------ the file
+    def generate(self) -> str:
+        body = self.block(self.prog.main, "    ")
+        kernels_src = [p._source if hasattr(p, "_source") else p.source() for p in self.plans]
+        # device buffers: every buffer a kernel or the host touches on the device
+        for p in self.plans:
+            for b in p.bufs.values():
+                self.device_bufs.setdefault(b.id, b)
+        externs = [b for b in self.prog.buffers if b.root is b and b.kind in ir.EXTERN_KINDS]
+        for b in externs:
+            self.dev(b)
+        for b in self.prog.buffers:
+            r = b.root
+            if r.init is not None and r.id in self.device_bufs:
+                self.mirror(r)
+        dev = sorted(self.device_bufs.values(), key=lambda b: b.id)
+        plan = A.plan_arena(self.prog, dev, self.full_writer, share=os.environ.get("ANVIL_HIP_SHARE", "1") != "0",
+                            fused=self.fused_group)
+        src = self.prog.source
+        name = src.display_path() if src is not None and hasattr(src, "display_path") else "<program>"
+        out = [f"// Generated by anvil (HIP backend) from {name} for MI355X ({ARCH}).",
+               f"// Build: hipcc --offload-arch={ARCH} -O3 -fPIC -shared -ffp-contract=off -munsafe-fp-atomics prog.hip -o prog.so -lz",
+               "", runtime_source(), "",
+               "// ---------------------------------------------------------------- buffers"]
+        for b in dev:
+            where = f"arena + {plan.offsets[b.id]}"
+            out.append(f"static {ctype(b.dtype)} *anvil_b{b.id};   // {b.kind} {b.name}{list(b.shape)} at {where}")
+        for bid in sorted(self.hosts):
+            b = self.by_id[bid]
+            out.append(f"static {ctype(b.dtype)} anvil_h{bid};   // host scalar {b.name}")
+        for b in sorted(self.mirrored.values(), key=lambda b: b.id):
+            out.append(f"static anvil_mirror anvil_mir{b.id};")
+        for b in self.prog.buffers:
+            r = b.root
+            if r is b and r.init is not None:
+                vals = ", ".join(flit(float(v)) if r.dtype == F32 else ilit(int(v)) for v in r.init)
+                out.append(f"static const {ctype(r.dtype)} anvil_init{r.id}[] = {{{vals}}};")
+        out += [""] + self.tables
+        out += ["", "// ---------------------------------------------------------------- kernels"]
+        out += kernels_src
+        out += ["", "// ---------------------------------------------------------------- profiling sites"]
+        sites = []
+        for p in self.plans:
+            fl, by = hip_cost.plan_cost(p)
+            sites.append(f"{{{c_string(p.name + ' ' + p.kind + ': ' + p.label)}, 0.0, 0, {float(fl)!r}, {float(by)!r}}}")
+        sites = sites or ['{"none", 0.0, 0, 0.0, 0.0}']
+        out.append(f"static anvil_site anvil_site_table[] = {{{', '.join(sites)}}};")
+        out += ["", "// ---------------------------------------------------------------- set-up"]
+        out.append("static void anvil_setup(void) {")
+        out.append("    if (anvil_dev.ready) return;")
+        out.append(f"    anvil_device_open({plan.size});")
+        for b in dev:
+            out.append(f"    anvil_b{b.id} = ({ctype(b.dtype)} *)(anvil_dev.arena + {plan.offsets[b.id]});")
+        for b in sorted(self.mirrored.values(), key=lambda b: b.id):
+            out.append(f"    anvil_mirror_init(&anvil_mir{b.id}, (void **)&anvil_b{b.id}, {max(4, 4 * b.numel)});")
+        for i, m in enumerate(self.faults, 1):
+            out.append(f"    anvil_fault_text[{i}] = {c_string(m)};")
+        out.append("    anvil_sites = anvil_site_table;")
+        out.append(f"    anvil_nsites = {len(self.plans)};")
+        out.append(f"    anvil_hs.seed0 = {self.seed}u;")
+        out.append("}")
+        out += ["", "// the state a run starts from: zeroed memory, constants uploaded, seed and stream reset",
+                "static void anvil_fresh(void) {",
+                "    anvil_arena_zero();"]
+        for b in dev:
+            r = b
+            if r.init is not None:
+                out.append(f"    memcpy(anvil_mir{r.id}.host, anvil_init{r.id}, sizeof anvil_init{r.id});")
+                out.append(f"    anvil_commit(&anvil_mir{r.id});")
+        for b in sorted(self.mirrored.values(), key=lambda b: b.id):
+            if b.init is None:
+                out.append(f"    anvil_mir{b.id}.valid = 0;")
+        for bid in sorted(self.hosts):
+            out.append(f"    anvil_h{bid} = 0;")
+        out += ["    anvil_hs.seed = anvil_hs.seed0;", "    anvil_hs.stream = 0;", "    anvil_hs.t0 = anvil_seconds();", "}"]
+        out += ["", "// ---------------------------------------------------------------- the program",
+                "static int anvil_program(void) {"]
+        for line in body:
+            if line.startswith("@@dirty "):
+                _, bid, ind = line.split(" ", 2)
+                if int(bid) in self.mirrored:
+                    out.append(f"{ind}anvil_mir{bid}.valid = 0;")
+                continue
+            out.append(line)
+        out += ["    goto anvil_end;", "anvil_end:", "    anvil_sync();", "    fflush(stdout);", "    return 0;", "}"]
+        out += self.abi(externs, plan)
+        return "\n".join(out) + "\n"
+
+    def fused_group(self, k):
+        got = self.group_of.get(k.id)
+        if got is None:
+            return None
+        plan = got
+        if len(plan.kernels) < 2:
+            return None
+        if not hasattr(plan, "_writes"):
+            plan._writes = plan.writes()
+        return id(plan), plan._writes
+
+    def full_writer(self, st, b) -> bool:
+        if isinstance(st, KernelStmt):
+            plan = self.plan_of.get(st.kernel.id)
+            k = st.kernel
+            if plan is not None:
+                plan = plan[0]
+                if any((k.id, i) in plan.skip_stores for i, s in enumerate(k.stmts)
+                       if isinstance(s, ir.Store) and s.buf.root is b):
+                    return False
+            return A._full_write(k, b)
+        if isinstance(st, ir.RTCall):
+            return st.name in A.RT_FULL_WRITES and st.args.get("buf") is not None and st.args["buf"].root is b
+        return False
+
+    def buffer_table(self) -> list[str]:
+        """anvil_buffer_read(id, dst, bytes): a buffer's current contents, for tests and tools."""
+        out = ["int anvil_buffer_read(int id, void *dst, long long bytes) {", "    switch (id) {"]
+        for b in sorted({x.root.id: x.root for x in self.prog.buffers}.values(), key=lambda b: b.id):
+            n = 4 * max(1, b.numel)
+            if self.is_host(b):
+                out.append(f"    case {b.id}: if (bytes < 4) return -2; memcpy(dst, &anvil_h{b.id}, 4); return 4;")
+            elif b.id in self.device_bufs:
+                out.append(f"    case {b.id}: if (bytes < {n}) return -2; anvil_to_host(dst, anvil_b{b.id}, {n}); return {n};")
+        out += ["    default: return -1;", "    }", "}"]
+        return out
+
+    def abi(self, externs, plan) -> list[str]:
+        ins = sorted([b for b in externs if b.kind == "input"], key=lambda b: b.name)
+        outs = sorted([b for b in externs if b.kind == "output"], key=lambda b: b.name)
+        out = ["", "// ---------------------------------------------------------------- C ABI", 'extern "C" {']
+        for b in ins + outs:
+            out.append(f"void *anvil_{sanitize(b.name)} = NULL;")
+            out.append(f"void *anvil_d{sanitize(b.name)} = NULL;")
+        out += [
+            "int anvil_init(void) { anvil_setup(); anvil_fresh(); return 0; }",
+            "int anvil_main(void) {",
+            "    anvil_setup();",
+            "    anvil_fresh();",
+            "    return anvil_program();",
+            "}",
+            "int anvil_entry(void) {",
+            "    if (!anvil_dev.ready) { anvil_setup(); anvil_fresh(); }",
+            "    anvil_hs.seed = anvil_hs.seed0; anvil_hs.stream = 0;"]
+        for b in ins:
+            out.append(f"    if (anvil_{sanitize(b.name)}) anvil_to_device(anvil_b{b.id}, anvil_{sanitize(b.name)}, {4 * b.numel});")
+            if b.id in self.mirrored:
+                out.append(f"    anvil_mir{b.id}.valid = 0;")
+        out.append("    const int rc = anvil_program();")
+        for b in outs:
+            out.append(f"    if (anvil_{sanitize(b.name)}) anvil_to_host(anvil_{sanitize(b.name)}, anvil_b{b.id}, {4 * b.numel});")
+        out += ["    return rc;", "}",
+                "// the same call with device pointers in the anvil_d<slot> variables: no copies",
+                "int anvil_entry_device(void) {",
+                "    if (!anvil_dev.ready) { anvil_setup(); anvil_fresh(); }",
+                "    anvil_device_barrier();",
+                "    anvil_hs.seed = anvil_hs.seed0; anvil_hs.stream = 0;"]
+        for b in ins + outs:
+            out.append(f"    {ctype(b.dtype)} *keep{b.id} = anvil_b{b.id};")
+            out.append(f"    if (anvil_d{sanitize(b.name)}) anvil_b{b.id} = ({ctype(b.dtype)} *)anvil_d{sanitize(b.name)};")
+            if b.id in self.mirrored:
+                out.append(f"    anvil_mir{b.id}.valid = 0;")
+        out.append("    const int rc = anvil_program();")
+        for b in ins + outs:
+            out.append(f"    anvil_b{b.id} = keep{b.id};")
+            if b.id in self.mirrored:
+                out.append(f"    anvil_mir{b.id}.valid = 0;")
+        out += ["    return rc;", "}"]
+        out += self.buffer_table()
+        out += [f"long long anvil_arena_bytes(void) {{ return {plan.size}LL; }}",
+                f"long long anvil_arena_unshared_bytes(void) {{ return {plan.size - plan.placed_bytes + plan.shared_bytes}LL; }}",
+                f"const char *anvil_target(void) {{ return {c_string('emulate' if self.emulate else ARCH)}; }}",
+                "}",
+                ""]
+        return out
+
+
+# ----------------------------------------------------------------------------- plugin API
+
+def generate(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False) -> str:
+    """The .hip source of a program (library=True: a function lowered by pyapi.lower, called
+    through anvil_entry with the input/output slots). emulate=True: a CPU build of the same
+    program for testing the generator on a machine without a GPU."""
+    return HipGen(prog, seed=seed, library=library, emulate=emulate).generate()
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise HipToolchainError("hipcc not found (ROCm is needed to build for MI355X; set $HIPCC)")
+
+
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-munsafe-fp-atomics", "-w",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def build(source: str, lib_path: str, emulate: bool = False) -> None:
+    """Compile a generated file into a shared library at lib_path (atomically)."""
+    d = tempfile.mkdtemp(prefix="anvil-hip-")
+    try:
+        src = os.path.join(d, "prog.hip")
+        with open(src, "w") as f:
+            f.write(source)
+        tmp = os.path.join(d, "prog.so")
+        if emulate:
+            cxx = os.environ.get("CXX") or shutil.which("g++") or shutil.which("c++")
+            if cxx is None:
+                raise HipToolchainError("no C++ compiler for the CPU build")
+            cmd = [cxx, "-O1", "-std=c++17", "-fwrapv", "-w", "-ffp-contract=off", "-DANVIL_EMULATE", "-fPIC",
+                   "-shared", "-x", "c++", src, "-o", tmp, "-lz"]
+        else:
+            cmd = [hipcc(), f"--offload-arch={ARCH}"] + HIP_FLAGS + [src, "-o", tmp, "-lz"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise HipToolchainError(f"{os.path.basename(cmd[0])} failed:\n{r.stderr[-4000:]}")
+        os.makedirs(os.path.dirname(os.path.abspath(lib_path)), exist_ok=True)
+        shutil.move(tmp, lib_path + ".tmp")
+        os.replace(lib_path + ".tmp", lib_path)
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def cache_dir() -> str:
+    """Where built libraries are kept: $ANVIL_CACHE, else the package's own _libs directory (so
+    libraries built on one machine travel with the source tree)."""
+    d = os.environ.get("ANVIL_CACHE") or os.path.join(os.path.dirname(HERE), "_libs")
+    os.makedirs(d, exist_ok=True)
+    return d
+
+
+def library_path(source: str, emulate: bool = False) -> str:
+    key = hashlib.sha256(source.encode()).hexdigest()[:20]
+    return os.path.join(cache_dir(), f"anvil-{key}{'-cpu' if emulate else ''}.so")
+
+
+_BUILD_LOCK = threading.Lock()
+
+
+def compile_source(source: str, emulate: bool = False, rebuild: bool = False) -> str:
+    lib = library_path(source, emulate)
+    with _BUILD_LOCK:
+        if rebuild or not os.path.exists(lib):
+            build(source, lib, emulate=emulate)
+    return lib
+
+
+class HipLibrary:
+    """A loaded generated library and its C ABI."""
+
+    def __init__(self, path: str, source: str | None = None):
+        self.path = path
+        self.source = source
+        self.lib = ctypes.CDLL(path)
+        for fn in ("anvil_main", "anvil_entry", "anvil_entry_device", "anvil_init", "anvil_sync_device",
+                   "anvil_profile_count", "anvil_marks_count"):
+            getattr(self.lib, fn).restype = ctypes.c_int
+        self.lib.anvil_profile_ms.restype = ctypes.c_double
+        self.lib.anvil_profile_ms.argtypes = [ctypes.c_int]
+        self.lib.anvil_profile_calls.restype = ctypes.c_long
+        self.lib.anvil_profile_calls.argtypes = [ctypes.c_int]
+        self.lib.anvil_profile_flops.restype = ctypes.c_double
+        self.lib.anvil_profile_flops.argtypes = [ctypes.c_int]
+        self.lib.anvil_profile_bytes.restype = ctypes.c_double
+        self.lib.anvil_profile_bytes.argtypes = [ctypes.c_int]
+        self.lib.anvil_profile_label.restype = ctypes.c_char_p
+        self.lib.anvil_profile_label.argtypes = [ctypes.c_int]
+        self.lib.anvil_profile_enable.argtypes = [ctypes.c_int]
+        self.lib.anvil_marks_select.argtypes = [ctypes.c_char_p]
+        self.lib.anvil_marks_elapsed_ms.restype = ctypes.c_double
+        self.lib.anvil_marks_elapsed_ms.argtypes = [ctypes.c_int, ctypes.c_int]
+        self.lib.anvil_arena_bytes.restype = ctypes.c_longlong
+        self.lib.anvil_target.restype = ctypes.c_char_p
+        self.lock = threading.Lock()
+
+    def slot(self, name: str) -> ctypes.c_void_p:
+        return ctypes.c_void_p.in_dll(self.lib, f"anvil_{name}")
+
+    def main(self) -> int:
+        return self.lib.anvil_main()
+
+    def profile(self) -> list[tuple[str, float, int, float, float]]:
+        """Per launch site: (label, total ms, launches, FLOPs per launch, bytes per launch)."""
+        self.lib.anvil_sync_device()
+        n = self.lib.anvil_profile_count()
+        return [(self.lib.anvil_profile_label(i).decode(), self.lib.anvil_profile_ms(i),
+                 self.lib.anvil_profile_calls(i), self.lib.anvil_profile_flops(i),
+                 self.lib.anvil_profile_bytes(i)) for i in range(n)]
+
+
+def load(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False,
+         rebuild: bool = False) -> HipLibrary:
+    src = generate(prog, seed=seed, library=library, emulate=emulate)
+    return HipLibrary(compile_source(src, emulate=emulate, rebuild=rebuild), src)

@@ -1,0 +1,433 @@
+"""Program analyses the HIP generator relies on.
+
+- read/write sets of statements (what a kernel, a loop or a run-time call touches);
+- `parallel_safe`: may every output element of a kernel run in its own thread, in any order? The
+  same question the reference's CUDA emitter asks (cuda.py:380-395, 618-633): plain stores must be
+  injective over the domain and free of gathers, and a kernel may read a buffer it writes only at the
+  element it writes;
+- `host_scalars`: the 0-d buffers that only the host computes (loop counters, and results of scalar
+  kernels that read only such values and constants), found by iterating to a fixed point, as the
+  reference's Metal backend does (metal.py:365-432). Kernels get them by value, so a training loop
+  needs no device round trip for its counters, its `if step >= N: break` or Adam's step count;
+- `plan_arena`: byte offsets of every device buffer in one allocation; temporaries whose lifetimes
+  do not overlap share bytes (the reference's arena.py:1-144 lifetime rule: a lifetime that touches
+  a loop covers the whole loop, and only buffers whose first use writes all of them take part).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+from .. import ir
+from ..ir import Buffer, Gather, Index, KernelStmt, Load, ScalarRef, Var
+
+# Run-time calls: which arguments they read and write (the reference's optimize.py:20-32 tables).
+RT_READS = {"shuffle": ("buf",), "show": ("buf",), "sleep": ("buf",), "nonzero": ("src",), "save": ("bufs",),
+            "save_npy": ("buf",)}
+RT_WRITES = {"load_idx": ("buf",), "load_csv": ("buf",), "load_bytes": ("buf",), "load_npy": ("buf",),
+             "iota": ("buf",), "iota_once": ("buf",), "shuffle": ("buf",), "clock": ("buf",), "nonzero": ("buf",),
+             "input": ("buf",), "load": ("bufs", "buf")}
+RT_FULL_WRITES = ("nonzero", "input", "clock", "iota", "iota_once", "load_idx", "load_csv", "load_bytes",
+                  "load_npy")
+ARENA_ALIGN = 256
+_UNSHARED = set(filter(None, __import__("os").environ.get("ANVIL_HIP_UNSHARED", "").split(",")))
+SHARED_KINDS = ("temp", "grad")
+
+
+def rt_args(st, table) -> list:
+    out = []
+    for key in table.get(st.name, ()):
+        v = st.args.get(key)
+        if v is None:
+            continue
+        out.extend(v if isinstance(v, list) else [v])
+    return [b for b in out if isinstance(b, Buffer)]
+
+
+# ----------------------------------------------------------------------------- loads and offsets
+
+def offset_loads(a: ir.Affine, out: list) -> None:
+    for g in a.gathers():
+        out.append(g.load)
+        offset_loads(g.load.offset, out)
+
+
+def kernel_loads(k: ir.Kernel) -> list:
+    """Every load of k: in its expressions, in their offsets' gathers, and in its stores' offsets."""
+    out = []
+    for e in k.exprs():
+        for x in ir.iter_expr(e):
+            if isinstance(x, Load):
+                out.append(x)
+            elif isinstance(x, Index):
+                offset_loads(x.affine, out)
+    for st in k.stores:
+        offset_loads(st.offset, out)
+    return out
+
+
+def affine_scalars(a: ir.Affine, out: set) -> None:
+    for t in a.terms:
+        if isinstance(t, ScalarRef):
+            out.add(t.buf.root)
+        elif isinstance(t, Gather):
+            affine_scalars(t.load.offset, out)
+            if t.rest is not None:
+                affine_scalars(t.rest, out)
+
+
+def kernel_reads(k: ir.Kernel) -> set:
+    out = {ld.buf.root for ld in kernel_loads(k)}
+    for e in k.exprs():
+        for x in ir.iter_expr(e):
+            if isinstance(x, Load):
+                affine_scalars(x.offset, out)
+            elif isinstance(x, Index):
+                affine_scalars(x.affine, out)
+    for st in k.stores:
+        affine_scalars(st.offset, out)
+        if st.accumulate:
+            out.add(st.buf.root)
+    return out
+
+
+def kernel_writes(k: ir.Kernel) -> set:
+    return {st.buf.root for st in k.stores}
+
+
+def stmt_reads(st) -> set:
+    if isinstance(st, KernelStmt):
+        return kernel_reads(st.kernel)
+    out: set = set()
+    if isinstance(st, ir.For):
+        for b in (st.start, st.stop):
+            if isinstance(b, Buffer):
+                out.add(b.root)
+        out |= block_reads(st.body)
+    elif isinstance(st, ir.While):
+        out |= block_reads(st.cond_block) | block_reads(st.body)
+        out.add(st.cond.root)
+    elif isinstance(st, ir.If):
+        out.add(st.cond.root)
+        out |= block_reads(st.then) | block_reads(st.orelse)
+    elif isinstance(st, ir.Print):
+        out |= {it.buf.root for it in st.items if it.buf is not None}
+    elif isinstance(st, ir.Check):
+        affine_scalars(st.value, out)
+    elif isinstance(st, ir.RTCall):
+        out |= {b.root for b in rt_args(st, RT_READS)}
+    return out
+
+
+def stmt_writes(st) -> set:
+    if isinstance(st, KernelStmt):
+        return kernel_writes(st.kernel)
+    out: set = set()
+    if isinstance(st, ir.For):
+        out.add(st.counter.root)
+        out |= block_writes(st.body)
+    elif isinstance(st, ir.While):
+        out |= block_writes(st.cond_block) | block_writes(st.body)
+    elif isinstance(st, ir.If):
+        out |= block_writes(st.then) | block_writes(st.orelse)
+    elif isinstance(st, ir.RTCall):
+        out |= {b.root for b in rt_args(st, RT_WRITES)}
+    return out
+
+
+def block_reads(b: ir.Block) -> set:
+    out: set = set()
+    for st in b.stmts:
+        out |= stmt_reads(st)
+    return out
+
+
+def block_writes(b: ir.Block) -> set:
+    out: set = set()
+    for st in b.stmts:
+        out |= stmt_writes(st)
+    return out
+
+
+# ----------------------------------------------------------------------------- parallel safety
+
+def injective_over(off: ir.Affine, vars_) -> bool:
+    """Distinct values of vars_ give distinct offsets: sorted by |coefficient|, each var's step must
+    exceed everything the smaller ones reach (a sufficient, exact-for-row-major test)."""
+    steps = []
+    for v in vars_:
+        if v.extent <= 1:
+            continue
+        c = abs(off.coef(v))
+        if c == 0:
+            return False
+        steps.append((c, v.extent))
+    reach = 0
+    for c, n in sorted(steps):
+        if c <= reach:
+            return False
+        reach += c * (n - 1)
+    return True
+
+
+def parallel_safe(k: ir.Kernel) -> bool:
+    written = {}
+    for st in k.stores:
+        written.setdefault(st.buf.root, []).append(st)
+        if st.accumulate:
+            continue                                    # an atomic add
+        if st.offset.gathers():
+            return False                                # duplicate indices: the last write wins
+        if not injective_over(st.offset, k.domain):
+            return False
+    for ld in kernel_loads(k):
+        stores = written.get(ld.buf.root)
+        if stores and any(s.accumulate or s.offset != ld.offset for s in stores):
+            return False                                # reads what another element writes
+    return True
+
+
+# ----------------------------------------------------------------------------- host scalars
+
+def is_scalar_kernel(k: ir.Kernel) -> bool:
+    return (not k.domain and k.red is None and not k.uses_rand()
+            and all(not st.buf.shape and not st.accumulate for st in k.stores))
+
+
+def host_scalars(prog: ir.Program) -> set:
+    """Ids of the 0-d buffers that live on the host only."""
+    writers: dict[int, list] = {}
+    counters = set()
+    for blk in ir.walk_blocks(prog.main):
+        for st in blk.stmts:
+            if isinstance(st, ir.For):
+                counters.add(st.counter.root.id)
+                writers.setdefault(st.counter.root.id, []).append("loop")
+            elif isinstance(st, KernelStmt):
+                for s in st.kernel.stores:
+                    writers.setdefault(s.buf.root.id, []).append(st.kernel)
+            elif isinstance(st, ir.RTCall):
+                for b in rt_args(st, RT_WRITES):
+                    writers.setdefault(b.root.id, []).append("rt")
+    by_id = {b.root.id: b.root for b in prog.buffers}
+
+    def eligible(bid) -> bool:
+        b = by_id.get(bid)
+        return b is not None and not b.shape and b.kind not in ir.EXTERN_KINDS
+
+    hosts = {c for c in counters if eligible(c) and all(w == "loop" for w in writers.get(c, []))}
+    scalar_ks = [k for k in ir.all_kernels(prog) if is_scalar_kernel(k)]
+
+    def outs(k):
+        return {st.buf.root.id for st in k.stores}
+
+    def reads_ok(k, allowed) -> bool:
+        for b in kernel_reads(k):
+            if b.id not in allowed and b.kind != "const":
+                return False
+        return True
+
+    banned: set = set()
+    changed = True
+    while changed:
+        changed = False
+        for k in scalar_ks:
+            if not reads_ok(k, hosts | (outs(k) - banned)):
+                continue
+            for o in outs(k) - hosts - banned:
+                ws = writers.get(o, [])
+                if eligible(o) and all(isinstance(w, ir.Kernel) and is_scalar_kernel(w) for w in ws):
+                    hosts.add(o)
+                    changed = True
+        for o in sorted(hosts - counters):
+            ws = writers.get(o, [])
+            if not all(isinstance(w, ir.Kernel) and reads_ok(w, hosts) and outs(w) <= hosts for w in ws):
+                hosts.discard(o)
+                banned.add(o)
+                changed = True
+    return hosts
+
+
+def is_host_kernel(k: ir.Kernel, hosts: set) -> bool:
+    if not is_scalar_kernel(k) or not k.stores:
+        return False
+    if any(st.buf.root.id not in hosts for st in k.stores):
+        return False
+    return all(b.id in hosts or b.kind == "const" for b in kernel_reads(k))
+
+
+# ----------------------------------------------------------------------------- program-wide reads
+
+def all_readers(prog: ir.Program) -> dict:
+    """buffer id -> number of statements (kernels, prints, calls, conditions) that read it."""
+    out: dict[int, int] = {}
+
+    def note(bs):
+        for b in bs:
+            out[b.id] = out.get(b.id, 0) + 1
+
+    def walk(blk):
+        for st in blk.stmts:
+            if isinstance(st, ir.For):
+                note({b.root for b in (st.start, st.stop) if isinstance(b, Buffer)})
+                note({st.counter.root})
+                walk(st.body)
+            elif isinstance(st, ir.While):
+                walk(st.cond_block)
+                note({st.cond.root})
+                walk(st.body)
+            elif isinstance(st, ir.If):
+                note({st.cond.root})
+                walk(st.then)
+                walk(st.orelse)
+            else:
+                note(stmt_reads(st))
+    walk(prog.main)
+    return out
+
+
+# ----------------------------------------------------------------------------- the arena
+
+@dataclass
+class ArenaPlan:
+    offsets: dict = field(default_factory=dict)     # buffer id -> byte offset
+    size: int = 0
+    shared_bytes: int = 0                            # what the shared buffers would take apart
+    placed_bytes: int = 0
+
+
+def _full_write(k: ir.Kernel, b: Buffer) -> bool:
+    """Does kernel k write every element of b (with plain stores)?"""
+    for st in k.stores:
+        if st.buf.root is not b or st.accumulate or st.offset.scalars() or st.offset.gathers():
+            continue
+        if st.offset.const != 0:
+            continue
+        n = ir.prod(v.extent for v in k.domain)
+        if n != b.numel or not injective_over(st.offset, k.domain):
+            continue
+        lo, hi = st.offset.var_bounds()
+        if lo == 0 and hi == b.numel - 1:
+            return True
+    return False
+
+
+def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = True, fused=None) -> ArenaPlan:
+    """Offsets for device_bufs. full_writer(stmt, buf) says whether a statement writes all of buf.
+    fused(kernel) -> (group key, buffers the group writes) or None: the kernels of one generated
+    kernel run together, so they are one position of the program (reads of what the group itself
+    writes are of the lane's own elements and do not start a lifetime early).
+    share=False gives every buffer its own bytes ($ANVIL_HIP_SHARE=0: for inspecting temporaries)."""
+    uses: dict[int, list] = {}
+    loops: list[tuple[int, int]] = []
+    pos = 0
+    by_id = {b.id: b for b in device_bufs}
+
+    def note(b, chain, write=False, full=False):
+        if b.id in by_id:
+            uses.setdefault(b.id, []).append((pos, chain, write, full))
+
+    def block(blk, chain):
+        for st in blk.stmts:
+            stmt(st, chain)
+
+    def stmt(st, chain):
+        nonlocal pos
+        pos += 1
+        if isinstance(st, ir.For):
+            start = pos
+            for b in (st.start, st.stop):
+                if isinstance(b, Buffer):
+                    note(b.root, chain)
+            note(st.counter.root, chain, write=True)
+            block(st.body, chain + (("loop", id(st)),))
+            pos += 1
+            loops.append((start, pos))
+        elif isinstance(st, ir.While):
+            start = pos
+            inner = chain + (("loop", id(st)),)
+            block(st.cond_block, inner)
+            pos += 1
+            note(st.cond.root, inner)
+            block(st.body, inner)
+            pos += 1
+            loops.append((start, pos))
+        elif isinstance(st, ir.If):
+            note(st.cond.root, chain)
+            block(st.then, chain + (("then", id(st)),))
+            block(st.orelse, chain + (("else", id(st)),))
+            pos += 1
+        elif isinstance(st, (ir.Break, ir.Continue)):
+            pass
+        else:
+            group = fused(st.kernel) if fused is not None and isinstance(st, KernelStmt) else None
+            own: set = set()
+            if group is not None:
+                key, own = group
+                if last_group[0] == key:
+                    pos -= 1                            # a later stage of the kernel just noted
+                last_group[0] = key
+            else:
+                last_group[0] = None
+            for b in stmt_reads(st):
+                if b not in own:
+                    note(b, chain)
+            for b in stmt_writes(st):
+                note(b, chain, write=True, full=full_writer(st, b))
+    last_group = [None]
+    block(prog.main, ())
+
+    def lifetime(us):
+        us = sorted(us, key=lambda u: u[0])
+        first = us[0][0]
+        at_first = [u for u in us if u[0] == first]
+        if any(not u[2] for u in at_first) or not any(u[3] for u in at_first):
+            return None                                 # read before it is all written
+        chain = at_first[0][1]
+        if any(u[1][:len(chain)] != chain for u in us):
+            return None                                 # the first write might not have run
+        lo, hi = first, us[-1][0]
+        grown = True
+        while grown:
+            grown = False
+            for a, b in loops:
+                if lo <= b and a <= hi and (a < lo or b > hi) and not (a <= lo and hi <= b):
+                    lo, hi = min(lo, a), max(hi, b)
+                    grown = True
+        return lo, hi
+
+    def rounded(b):
+        return max(ARENA_ALIGN, (b.nbytes + ARENA_ALIGN - 1) // ARENA_ALIGN * ARENA_ALIGN)
+
+    plan = ArenaPlan()
+    fixed, shared = [], []
+    for b in device_bufs:
+        span = None
+        if share and b.kind in SHARED_KINDS and not getattr(b, "heap", False) and b.id in uses \
+                and str(b.id) not in _UNSHARED:
+            span = lifetime(uses[b.id])
+        if span is None:
+            fixed.append(b)
+        else:
+            shared.append((b, span, rounded(b)))
+    off = 0
+    for b in sorted(fixed, key=lambda b: b.id):
+        plan.offsets[b.id] = off
+        off += rounded(b)
+    base = off
+    shared.sort(key=lambda it: (-it[2], it[1][0], it[0].id))
+    placed = []
+    top = 0
+    for b, (lo, hi), n in shared:
+        busy = sorted((o, o + s) for (l2, h2, o, s) in placed if l2 <= hi and lo <= h2)
+        o = 0
+        for s, e in busy:
+            if o + n <= s:
+                break
+            o = max(o, e)
+        placed.append((lo, hi, o, n))
+        plan.offsets[b.id] = base + o
+        top = max(top, o + n)
+    plan.shared_bytes = sum(n for _, _, n in shared)
+    plan.placed_bytes = top
+    plan.size = base + top
+    return plan

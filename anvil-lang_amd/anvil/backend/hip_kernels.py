@@ -1,0 +1,726 @@
+"""Kernel schedules: how one IR kernel (or a run of them) becomes one HIP kernel.
+
+  map     no reduction: a grid-stride loop, one output element per lane and step.
+  serial  a kernel whose outputs must be produced in order (cuda.py:380-395): one lane does all.
+  rows    L lanes per output row (L = 1, 64 = one wavefront, or 256 = one workgroup). The row's
+          elements are split over the lanes, each lane reduces its share, and the lanes' partial
+          results are combined with cross-lane shuffles (and LDS across the four waves of a
+          workgroup). Several consecutive IR kernels over the same rows (softmax's max, exp-sum and
+          divide; layer norm's mean, variance and normalize; cross-entropy's log-softmax) become
+          the stages of one kernel: per-row results stay in registers, and each lane keeps its
+          share of a row in registers between stages, so the row is read from memory once.
+  split   a reduction whose elements are strided in memory (a bias gradient, Σ_i dY[i, j]): the
+          lanes of a wavefront take neighbouring outputs (coalesced loads) and a workgroup splits
+          each output's reduction TY ways, combining the partial results through LDS in a fixed
+          order.
+
+Each plan produces the kernel's source and the host-side launch: grid, block and arguments.
+"""
+from __future__ import annotations
+
+from .. import ir
+from ..ir import F32, I32, Gather, Load, ScalarRef, Var
+from . import hip_analysis as A
+from .hip_emit import Emitter, Scope, ctype, flit, ilit
+
+THREADS = 256
+MAX_BLOCKS = 1 << 16
+QMAX = 16                       # register-cached elements per lane and row
+CACHE_REGS = 96                 # register budget for cached row elements, per lane
+CU_WAVES = 256 * 4              # waves that fill the chip once (256 CUs x 4 SIMDs)
+
+
+def index_type(n: int) -> str:
+    return "uint32_t" if n < (1 << 31) else "uint64_t"
+
+
+def decode(vars_, src: str, it: str) -> list[str]:
+    """C declarations of each var from a flattened row-major index."""
+    out = []
+    strides = ir.row_major_strides([v.extent for v in vars_])
+    for k, (v, s) in enumerate(zip(vars_, strides)):
+        expr = src if s == 1 else f"({src}) / {s}u"
+        if k > 0 and v.extent > 1:
+            expr = f"({expr}) % {v.extent}u"
+        if v.extent == 1:
+            expr = "0"
+        out.append(f"const int v{v.id} = (int)({expr});")
+    return out
+
+
+def red_init(op: str, dtype: str) -> str:
+    if op in ("sum",):
+        return "0.0f" if dtype == F32 else "0"
+    if op == "prod":
+        return "1.0f" if dtype == F32 else "1"
+    if op in ("max", "argmax"):
+        return "(-__builtin_inff())" if dtype == F32 else "(-2147483647 - 1)"
+    return "__builtin_inff()" if dtype == F32 else "2147483647"
+
+
+def red_combine(op: str, dtype: str, a: str, b: str) -> str:
+    if op == "sum":
+        return f"({a} + {b})" if dtype == F32 else f"anvil_wrap_add({a}, {b})"
+    if op == "prod":
+        return f"({a} * {b})" if dtype == F32 else f"anvil_wrap_mul({a}, {b})"
+    if op == "max":
+        return f"anvil_maxf({a}, {b})" if dtype == F32 else f"anvil_maxi({a}, {b})"
+    return f"anvil_minf({a}, {b})" if dtype == F32 else f"anvil_mini({a}, {b})"
+
+
+RED_CODE = {"sum": "ANVIL_RED_SUM", "prod": "ANVIL_RED_PROD", "max": "ANVIL_RED_MAX", "min": "ANVIL_RED_MIN"}
+
+
+class KernelScope(Scope):
+    """Device code of one plan: buffers and host scalars become parameters as they are used."""
+
+    def __init__(self, plan: "Plan"):
+        self.plan = plan
+        self.names: dict = {}
+        self.acc_name = "acc"
+        self.rand = "u"
+        self.stream_name = "anvil_rs0"
+        self.fwd: dict = {}               # canonical (buffer id, offset) -> C expression of its value
+        self.canon = None                 # var -> canonical symbol, for forwarding
+
+    def var(self, v):
+        return self.names.get(v, f"v{v.id}")
+
+    def buf(self, b):
+        return self.plan.use_buf(b.root)
+
+    def host_scalar(self, b):
+        if b.root.id in self.plan.gen.hosts:
+            return self.plan.use_host(b.root)
+        return None
+
+    def acc(self):
+        return self.acc_name
+
+    def rand_index(self):
+        return self.rand
+
+    def stream(self):
+        return self.stream_name
+
+    def fault(self, message):
+        return self.plan.gen.fault(message)
+
+    def override_load(self, ld):
+        if self.canon is None or not self.fwd:
+            return None
+        key = canon_key(ld.buf, ld.offset, self.canon)
+        if key is None:
+            return None
+        got = self.fwd.get(key)
+        if callable(got):
+            return got(ld)
+        return got
+
+
+def canon_key(buf, off: ir.Affine, canon: dict):
+    terms = []
+    for t, c in off.terms.items():
+        if not isinstance(t, Var) or t not in canon:
+            return None
+        terms.append((canon[t], c))
+    return (buf.root.id, off.const, tuple(sorted(terms)))
+
+
+class Plan:
+    """One generated kernel: its name, source and launch."""
+
+    kind = "?"
+
+    def __init__(self, gen, kernels, name: str):
+        self.gen = gen
+        self.kernels = kernels
+        self.name = name
+        self.bufs: dict[int, ir.Buffer] = {}
+        self.hosts: dict[int, ir.Buffer] = {}
+        self.streams = [k for k in kernels if k.uses_rand()]
+        self.skip_stores: set = set()      # (kernel id, store index) of dead stores
+        self.label = " + ".join(k.label or k.name for k in kernels)
+
+    # parameters
+    def use_buf(self, b) -> str:
+        self.bufs.setdefault(b.id, b)
+        return f"b{b.id}"
+
+    def use_host(self, b) -> str:
+        self.hosts.setdefault(b.id, b)
+        return f"h{b.id}"
+
+    def params(self) -> str:
+        ps = [f"uint32_t anvil_rs{i}" for i in range(max(1, len(self.streams)))] + ["uint32_t anvil_seed"]
+        ps += [f"{ctype(b.dtype)} h{b.id}" for b in self.hosts.values()]
+        ps += [f"{ctype(b.dtype)} *__restrict__ b{b.id}" for b in self.bufs.values()]
+        return ", ".join(ps)
+
+    def launch_args(self, stream_vars: list) -> list:
+        sv = stream_vars or ["0u"]
+        args = list(sv) + ["anvil_hs.seed"]
+        args += [f"anvil_h{b.id}" for b in self.hosts.values()]
+        args += [f"anvil_b{b.id}" for b in self.bufs.values()]
+        return args
+
+    def stream_param(self, k) -> str:
+        return f"anvil_rs{self.streams.index(k)}" if k in self.streams else "anvil_rs0"
+
+    def writes(self) -> set:
+        out = set()
+        for k in self.kernels:
+            out |= A.kernel_writes(k)
+        return out
+
+    def comment(self) -> str:
+        parts = []
+        for k in self.kernels:
+            d = " x ".join(f"{v.name}<{v.extent}" for v in k.domain) or "scalar"
+            r = f" reduce {k.red.op} " + " x ".join(f"{v.name}<{v.extent}" for v in k.red.vars) if k.red else ""
+            parts.append(f"{k.name} [{d}]{r}")
+        return f"// {self.kind}: " + "; ".join(parts)
+
+    def header(self, threads: int) -> str:
+        return f"__global__ void __launch_bounds__({threads}) {self.name}({self.params()})"
+
+    # body helpers
+    def statements(self, em: Emitter, k: ir.Kernel, scope: KernelScope, parallel: bool, guard: str | None = None,
+                   on_store=None) -> None:
+        for i, st in enumerate(k.stmts):
+            if isinstance(st, ir.Let):
+                em.let(st)
+                continue
+            val = em.store_value(st)
+            if (k.id, i) in self.skip_stores:
+                if on_store:
+                    on_store(st, val)
+                em.reset_memo()
+                continue
+            off = em.affine(st.offset, st.buf)
+            target = f"{scope.buf(st.buf)}[{off}]"
+            if st.accumulate:
+                if parallel:
+                    line = f"atomicAdd(&{target}, {val});"
+                elif st.buf.dtype == I32:
+                    line = f"{target} = anvil_wrap_add({target}, {val});"
+                else:
+                    line = f"{target} += {val};"
+            else:
+                line = f"{target} = {val};"
+            em.emit(f"if ({guard}) {line}" if guard else line)
+            if on_store:
+                on_store(st, val)
+            em.reset_memo()
+
+
+# ----------------------------------------------------------------------------- map
+
+class MapPlan(Plan):
+    kind = "map"
+
+    def __init__(self, gen, k, name):
+        super().__init__(gen, [k], name)
+        self.k = k
+        self.total = ir.prod(v.extent for v in k.domain)
+        self.threads = THREADS
+        self.blocks = max(1, min(-(-self.total // THREADS), MAX_BLOCKS))
+
+    def source(self) -> str:
+        k = self.k
+        it = index_type(self.total)
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(k)
+        body: list[str] = []
+        em = Emitter(sc, body, "        ")
+        for line in decode(k.domain, "u", it):
+            em.emit(line)
+        self.statements(em, k, sc, parallel=True)
+        head = [self.comment(), self.header(self.threads) + " {",
+                f"    for ({it} u = ({it})blockIdx.x * {self.threads}u + threadIdx.x; u < {self.total}u; "
+                f"u += ({it})gridDim.x * {self.threads}u) {{"]
+        return "\n".join(head + body + ["    }", "}"])
+
+    def grid(self):
+        return self.blocks, self.threads
+
+
+# ----------------------------------------------------------------------------- serial
+
+class SerialPlan(Plan):
+    kind = "serial"
+
+    def __init__(self, gen, k, name):
+        super().__init__(gen, [k], name)
+        self.k = k
+        self.total = ir.prod(v.extent for v in k.domain)
+
+    def source(self) -> str:
+        k = self.k
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(k)
+        body: list[str] = []
+        em = Emitter(sc, body, "        ")
+        for line in decode(k.domain, "u", "uint64_t"):
+            em.emit(line)
+        if k.red is not None:
+            serial_reduction(em, sc, k, "        ")
+        self.statements(em, k, sc, parallel=False)
+        head = [self.comment(), self.header(1) + " {",
+                f"    for (uint64_t u = 0; u < {self.total}ull; u++) {{"]
+        return "\n".join(head + body + ["    }", "}"])
+
+    def grid(self):
+        return 1, 1
+
+
+def serial_reduction(em: Emitter, sc: KernelScope, k: ir.Kernel, ind: str) -> None:
+    """The reduction as nested loops in one lane (element order = the flattened row-major order)."""
+    red = k.red
+    op, dt = red.op, red.body.dtype
+    T = ctype(dt)
+    arg = op in ("argmax", "argmin")
+    if arg:
+        em.emit(f"{T} best = {red_init(op, dt)}; int acc = 2147483647; int ridx = 0;")
+    else:
+        em.emit(f"{T} acc = {red_init(op, dt)};")
+    saved_ind = em.ind
+    for v in red.vars:
+        em.emit(f"for (int v{v.id} = 0; v{v.id} < {v.extent}; v{v.id}++) {{")
+        em.ind += "    "
+    saved = em.memo
+    em.memo = dict(saved)
+    val = em.ex(red.body)
+    if arg:
+        em.emit(f"if ({val} {'>' if op == 'argmax' else '<'} best || ({val} == best && ridx < acc)) "
+                f"{{ best = {val}; acc = ridx; }}")
+        em.emit("ridx++;")
+    else:
+        em.emit(f"acc = {red_combine(op, dt, 'acc', val)};")
+    em.memo = saved
+    for _ in red.vars:
+        em.ind = em.ind[:-4]
+        em.emit("}")
+    em.ind = saved_ind
+
+
+# ----------------------------------------------------------------------------- rows
+
+class RowsPlan(Plan):
+    """Stages over the same rows; stage 0 is a reduction whose domain is the rows."""
+
+    kind = "rows"
+
+    def __init__(self, gen, kernels, name, lanes: int, emulate: bool):
+        super().__init__(gen, kernels, name)
+        head = kernels[0]
+        self.outer = list(head.domain)
+        self.inner_extents = [v.extent for v in head.red.vars]
+        self.R = ir.prod(v.extent for v in self.outer)
+        self.n = ir.prod(self.inner_extents)
+        self.L = lanes
+        self.Q = -(-self.n // lanes)
+        self.rpb = THREADS // lanes if lanes < THREADS else 1
+        self.threads = THREADS if lanes > 1 else min(THREADS, max(64, 64 * -(-self.R // 64)))
+        if lanes == 1:
+            self.rpb = self.threads
+        self.blocks = max(1, min(-(-self.R // self.rpb), MAX_BLOCKS))
+        self.cached = self.Q <= QMAX and (lanes > 1 or self.n <= 32)
+        self.cache_arrays: dict = {}       # canonical key -> array name
+        self.emulate = emulate
+        self.plan_cache()
+
+    # which element-level values live in registers between stages
+    def stage_vars(self, k):
+        if k.red is not None:
+            return list(k.domain), list(k.red.vars)
+        no = len(self.outer)
+        return list(k.domain[:no]), list(k.domain[no:])
+
+    def canon_map(self, k) -> dict:
+        outer, inner = self.stage_vars(k)
+        m = {v: ("o", i) for i, v in enumerate(outer)}
+        m.update({v: ("i", i) for i, v in enumerate(inner)})
+        return m
+
+    def plan_cache(self):
+        if not self.cached:
+            return
+        seen: dict = {}
+        written: dict = {}
+        for si, k in enumerate(self.kernels):
+            cm = self.canon_map(k)
+            _, inner = self.stage_vars(k)
+            inner_set = set(inner)
+            for ld in A.kernel_loads(k):
+                key = canon_key(ld.buf, ld.offset, cm)
+                if key is None or not any(v in inner_set for v in ld.offset.direct_vars()):
+                    continue
+                seen.setdefault(key, set()).add(si)
+            if k.red is None:
+                for st in k.stores:
+                    key = canon_key(st.buf, st.offset, cm)
+                    if key is not None:
+                        written[key] = si
+        budget = CACHE_REGS // max(1, self.Q)
+        for key, stages in sorted(seen.items(), key=lambda kv: (min(kv[1]), repr(kv[0]))):
+            if len(self.cache_arrays) >= budget:
+                break
+            if key in written or len(stages) >= 2:
+                self.cache_arrays[key] = f"c{len(self.cache_arrays)}"
+        for key in written:
+            if key not in self.cache_arrays and len(self.cache_arrays) < budget:
+                self.cache_arrays[key] = f"c{len(self.cache_arrays)}"
+
+    def source(self) -> str:
+        L, Q, n = self.L, self.Q, self.n
+        out = [self.comment() + f" · {L} lane(s) per row, {self.R} rows of {n}"]
+        body: list[str] = []
+        ind = "        "
+        shared: list[str] = []
+        sc = KernelScope(self)
+        em = Emitter(sc, body, ind)
+        if L == THREADS:
+            row0, rstep = "blockIdx.x", "gridDim.x"
+            pre = ["    const int lane = threadIdx.x;"]
+        elif L == 1:
+            row0, rstep = f"blockIdx.x * {self.rpb}u + threadIdx.x", f"gridDim.x * {self.rpb}u"
+            pre = ["    const int lane = 0;"]
+        else:
+            row0, rstep = f"blockIdx.x * {self.rpb}u + (threadIdx.x / {L}u)", f"gridDim.x * {self.rpb}u"
+            pre = [f"    const int lane = threadIdx.x % {L}u;"]
+        pre.append("    (void)lane;")
+        for line in decode(self.outer, "row", "uint32_t"):
+            em.emit(line)
+        for key, name in self.cache_arrays.items():
+            em.emit(f"{ctype(self._key_dtype(key))} {name}[{Q}];")
+        populated: set = set()
+        fwd: dict = {}
+        for si, k in enumerate(self.kernels):
+            em.reset_memo()
+            cm = self.canon_map(k)
+            # the canonical symbols of this stage's own vars: outer vars keep the head's names
+            for i, v in enumerate(self.stage_vars(k)[0]):
+                sc.names[v] = f"v{self.outer[i].id}"
+            sc.canon = cm
+            sc.stream_name = self.stream_param(k)
+            if k.red is not None:
+                self.reduction_stage(em, sc, k, si, shared, fwd, populated)
+            else:
+                self.map_stage(em, sc, k, si, fwd, populated)
+            populated |= {key for key in self.cache_arrays}
+        if L == THREADS:
+            em.emit("__syncthreads();")
+        text = out + [self.header(self.threads) + " {"] + pre + shared
+        text.append(f"    for (uint32_t row = {row0}; row < {self.R}u; row += {rstep}) {{")
+        return "\n".join(text + body + ["    }", "}"])
+
+    def _key_dtype(self, key):
+        bid = key[0]
+        for k in self.kernels:
+            for ld in A.kernel_loads(k):
+                if ld.buf.root.id == bid:
+                    return ld.buf.root.dtype
+            for st in k.stores:
+                if st.buf.root.id == bid:
+                    return st.buf.root.dtype
+        return F32
+
+    def element_loop(self, em: Emitter, inner_vars, body_fn):
+        """for q: j = lane + L*q; decode the inner vars; body_fn(q)."""
+        L, Q, n = self.L, self.Q, self.n
+        saved_memo = em.memo
+        if self.cached:
+            em.emit("#pragma unroll")
+            em.emit(f"for (int q = 0; q < {Q}; q++) {{")
+            em.ind += "    "
+            em.emit(f"const uint32_t j = (uint32_t)lane + {L}u * (uint32_t)q;")
+            if n % L:
+                em.emit(f"if (j < {n}u) {{")
+                em.ind += "    "
+        else:
+            em.emit(f"for (uint32_t j = (uint32_t)lane; j < {n}u; j += {L}u) {{")
+            em.ind += "    "
+        em.memo = dict(saved_memo)
+        for line in decode(inner_vars, "j", "uint32_t"):
+            em.emit(line)
+        body_fn()
+        em.memo = saved_memo
+        if self.cached and n % L:
+            em.ind = em.ind[:-4]
+            em.emit("}")
+        em.ind = em.ind[:-4]
+        em.emit("}")
+
+    def install_cache(self, sc: KernelScope, cm, fwd: dict, populated: set, em: Emitter):
+        """Forwarded row values, and cached element values (loaded on first use)."""
+        table = dict(fwd)
+        for key, name in self.cache_arrays.items():
+            if key in populated or key in fwd:
+                table[key] = fwd.get(key, f"{name}[q]")
+            else:
+                def first_load(ld, name=name, key=key):
+                    v = em.build(ld)
+                    em.emit(f"{name}[q] = {v};")
+                    return f"{name}[q]"
+                table[key] = first_load
+        sc.fwd = table
+
+    def reduction_stage(self, em, sc, k, si, shared, fwd, populated):
+        red = k.red
+        op, dt = red.op, red.body.dtype
+        T = ctype(dt)
+        arg = op in ("argmax", "argmin")
+        cm = self.canon_map(k)
+        sc.rand = "row"
+        self.install_cache(sc, cm, fwd, populated, em)
+        if arg:
+            em.emit(f"{T} best{si} = {red_init(op, dt)}; int acc{si} = 2147483647;")
+        else:
+            em.emit(f"{T} acc{si} = {red_init(op, dt)};")
+
+        def body():
+            val = em.ex(red.body)
+            if arg:
+                em.emit(f"if ({val} {'>' if op == 'argmax' else '<'} best{si} || ({val} == best{si} && (int)j < acc{si})) "
+                        f"{{ best{si} = {val}; acc{si} = (int)j; }}")
+            else:
+                em.emit(f"acc{si} = {red_combine(op, dt, f'acc{si}', val)};")
+        self.element_loop(em, list(red.vars), body)
+        if self.L == 64:
+            if arg:
+                em.emit(f"anvil_wave_arg<{'true' if op == 'argmax' else 'false'}, {T}>(best{si}, acc{si});")
+            else:
+                em.emit(f"acc{si} = anvil_wave_all<{RED_CODE[op]}, {T}>(acc{si});")
+        elif self.L == THREADS:
+            if arg:
+                shared.append(f"    __shared__ {T} sv{si}[4]; __shared__ int si{si}[4];")
+                em.emit(f"anvil_block_arg<{'true' if op == 'argmax' else 'false'}, {T}>(best{si}, acc{si}, sv{si}, si{si});")
+            else:
+                shared.append(f"    __shared__ {T} sv{si}[4];")
+                em.emit(f"acc{si} = anvil_block_all<{RED_CODE[op]}, {T}>(acc{si}, sv{si});")
+        sc.acc_name = f"acc{si}"
+        sc.fwd = dict(fwd)
+        self.row_statements(em, sc, k, cm, fwd)
+
+    def row_statements(self, em, sc, k, cm, fwd):
+        def on_store(st, val):
+            key = canon_key(st.buf, st.offset, cm)
+            if key is not None and not st.accumulate:
+                fwd[key] = val
+                sc.fwd = dict(fwd)
+        self.statements(em, k, sc, parallel=True, guard="lane == 0" if self.L > 1 else None, on_store=on_store)
+
+    def map_stage(self, em, sc, k, si, fwd, populated):
+        cm = self.canon_map(k)
+        _, inner = self.stage_vars(k)
+        if not inner:                                   # a per-row scalar stage
+            sc.rand = "row"
+            sc.fwd = dict(fwd)
+            self.row_statements(em, sc, k, cm, fwd)
+            return
+        sc.rand = f"(row * {self.n}u + j)"
+        self.install_cache(sc, cm, fwd, populated, em)
+
+        def body():
+            def on_store(st, val):
+                key = canon_key(st.buf, st.offset, cm)
+                if key is None or st.accumulate:
+                    return
+                name = self.cache_arrays.get(key)
+                if name is not None:
+                    em.emit(f"{name}[q] = {val};")
+                    fwd[key] = f"{name}[q]"
+                    sc.fwd[key] = f"{name}[q]"
+            self.statements(em, k, sc, parallel=True, on_store=on_store)
+        self.element_loop(em, inner, body)
+
+    def grid(self):
+        return self.blocks, self.threads
+
+
+# ----------------------------------------------------------------------------- split
+
+class SplitPlan(Plan):
+    """TX outputs per workgroup, each reduced TY ways (lane t: output t % TX, share t / TX)."""
+
+    kind = "split"
+
+    def __init__(self, gen, k, name, ty: int):
+        super().__init__(gen, [k], name)
+        self.k = k
+        self.R = ir.prod(v.extent for v in k.domain)
+        self.n = ir.prod(v.extent for v in k.red.vars)
+        self.TY = ty
+        self.TX = THREADS // ty
+        self.blocks = max(1, min(-(-self.R // self.TX), MAX_BLOCKS))
+
+    def source(self) -> str:
+        k = self.k
+        red = k.red
+        op, dt = red.op, red.body.dtype
+        T = ctype(dt)
+        TX, TY = self.TX, self.TY
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(k)
+        sc.rand = "row"
+        body: list[str] = []
+        em = Emitter(sc, body, "        ")
+        for line in decode(k.domain, "row", "uint32_t"):
+            em.emit(line)
+        em.emit(f"{T} acc = {red_init(op, dt)};")
+        em.emit(f"if (row < {self.R}u) {{")
+        em.ind += "    "
+        em.emit(f"for (uint32_t j = ty; j < {self.n}u; j += {TY}u) {{")
+        em.ind += "    "
+        saved = em.memo
+        em.memo = dict(saved)
+        for line in decode(list(red.vars), "j", "uint32_t"):
+            em.emit(line)
+        val = em.ex(red.body)
+        em.emit(f"acc = {red_combine(op, dt, 'acc', val)};")
+        em.memo = saved
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        em.emit("part[ty][tx] = acc;")
+        em.emit("__syncthreads();")
+        em.emit(f"if (ty == 0 && row < {self.R}u) {{")
+        em.ind += "    "
+        em.emit("acc = part[0][tx];")
+        em.emit(f"for (int p = 1; p < {TY}; p++) acc = {red_combine(op, dt, 'acc', 'part[p][tx]')};")
+        self.statements(em, k, sc, parallel=True)
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        em.emit("__syncthreads();")
+        head = [self.comment() + f" · {TX} outputs x {TY}-way split per workgroup",
+                self.header(THREADS) + " {",
+                f"    __shared__ {T} part[{TY}][{TX}];",
+                f"    const uint32_t tx = threadIdx.x % {TX}u, ty = threadIdx.x / {TX}u;",
+                f"    for (uint32_t rb = blockIdx.x * {TX}u; rb < {self.R}u; rb += gridDim.x * {TX}u) {{",
+                "        const uint32_t row = rb + tx;"]
+        return "\n".join(head + body + ["    }", "}"])
+
+    def grid(self):
+        return self.blocks, THREADS
+
+
+# ----------------------------------------------------------------------------- choosing
+
+def inner_contiguous(k: ir.Kernel) -> bool:
+    """Do the reduction's loads walk memory with unit stride along its innermost variable?"""
+    if k.red is None or not k.red.vars:
+        return False
+    v = k.red.vars[-1]
+    unit = other = 0
+    for ld in ir.loads_in(k.red.body):
+        if not ld.buf.root.shape:
+            continue
+        c = ld.offset.coef(v)
+        if c == 1:
+            unit += 1
+        elif c != 0:
+            other += 1
+    return unit > 0 and unit >= other
+
+
+def rows_lanes(k: ir.Kernel, emulate: bool) -> int:
+    n = ir.prod(v.extent for v in k.red.vars)
+    R = ir.prod(v.extent for v in k.domain)
+    if emulate or n <= 32 or not inner_contiguous(k):
+        return 1
+    if n > 1024 or R < CU_WAVES // 4:
+        return THREADS
+    return 64
+
+
+def split_ways(k: ir.Kernel, emulate: bool) -> int:
+    """TY for a strided reduction (1: a plain rows kernel with one lane per output)."""
+    if emulate or k.red is None or k.red.op in ("argmax", "argmin"):
+        return 1
+    n = ir.prod(v.extent for v in k.red.vars)
+    R = ir.prod(v.extent for v in k.domain)
+    if n < 64 or inner_contiguous(k) or R >= 64 * CU_WAVES:
+        return 1
+    for ty in (16, 8, 4, 2):
+        if n >= 16 * ty:
+            return ty
+    return 1
+
+
+# ----------------------------------------------------------------------------- row groups
+
+class GroupBuilder:
+    """Decides which consecutive kernels can be stages of one rows kernel."""
+
+    def __init__(self, head: ir.Kernel):
+        self.kernels = [head]
+        self.outer_ext = [v.extent for v in head.domain]
+        self.inner_ext = [v.extent for v in head.red.vars]
+        self.stores: dict = {}          # buffer id -> canonical offset key of its stores
+        self.reads: dict = {}           # buffer id -> set of canonical offset keys read
+        self._note(head)
+
+    def canon(self, k):
+        if k.red is not None:
+            outer, inner = list(k.domain), list(k.red.vars)
+        else:
+            no = len(self.outer_ext)
+            outer, inner = list(k.domain[:no]), list(k.domain[no:])
+        m = {v: ("o", i) for i, v in enumerate(outer)}
+        m.update({v: ("i", i) for i, v in enumerate(inner)})
+        return m
+
+    def _note(self, k):
+        cm = self.canon(k)
+        for ld in A.kernel_loads(k):
+            self.reads.setdefault(ld.buf.root.id, set()).add(canon_key(ld.buf, ld.offset, cm))
+        for st in k.stores:
+            self.stores[st.buf.root.id] = canon_key(st.buf, st.offset, cm)
+
+    def fits(self, k: ir.Kernel, hosts: set) -> bool:
+        if A.is_host_kernel(k, hosts) or not A.parallel_safe(k):
+            return False
+        if any(st.accumulate or st.offset.gathers() for st in k.stores):
+            return False
+        if k.red is not None:
+            if [v.extent for v in k.domain] != self.outer_ext or [v.extent for v in k.red.vars] != self.inner_ext:
+                return False
+            if k.red.op in ("argmax", "argmin") and False:
+                return False
+        else:
+            no = len(self.outer_ext)
+            ext = [v.extent for v in k.domain]
+            if ext[:no] != self.outer_ext or ext[no:] not in ([], self.inner_ext):
+                return False
+        cm = self.canon(k)
+        # reads of what the group wrote must be the elements this lane wrote
+        for ld in A.kernel_loads(k):
+            bid = ld.buf.root.id
+            if bid in self.stores:
+                key = canon_key(ld.buf, ld.offset, cm)
+                if key is None or key != self.stores[bid]:
+                    return False
+        scal: set = set()
+        for e in k.exprs():
+            for x in ir.iter_expr(e):
+                if isinstance(x, Load):
+                    A.affine_scalars(x.offset, scal)
+        for st in k.stores:
+            A.affine_scalars(st.offset, scal)
+        if any(b.id in self.stores for b in scal):
+            return False
+        # no earlier stage may read what this one writes, and one place per buffer
+        for st in k.stores:
+            bid = st.buf.root.id
+            if bid in self.reads:
+                return False
+            key = canon_key(st.buf, st.offset, cm)
+            if key is None or (bid in self.stores and self.stores[bid] != key):
+                return False
+        return True
+
+    def add(self, k):
+        self.kernels.append(k)
+        self._note(k)

@@ -1,0 +1,158 @@
+#!/usr/bin/env python3
+"""Benchmark: config C2 of BASELINE.json through the HIP backend on one MI355X.
+
+The workload is the kernel IR of the 784-1024-1024-10 MLP training program (ReLU, cross-entropy,
+adam(lr=1e-3), batch 256, shuffled batches, 500 steps; X f32[65536, 784] ~ U[0,1), labels ~
+U{0..9}, Linear-default init after seed(1)) as the reference front end produces it
+(tests/golden/ir/c2_wide_mlp.json). The program generates its own synthetic data on the device.
+
+A step is one training iteration: the batch gather, forward, backward and Adam update. The library
+records a device event at the start of every iteration of the batch loop; the timed region is the K
+iterations after W warm-up ones, all on the library's stream, with the device synchronized before
+and after. `value` is samples/s over those K steps.
+
+The roofline object is for the generated kernel that takes the most device time in a second,
+profiled run of the same program (HIP events around every launch on the library's stream):
+achieved = its algorithmic FLOPs (or bytes) per launch / its mean launch time.
+
+cpu_baseline: this repository's NumPy interpreter of the same IR (oracle/interp.py, which follows
+the reference interpreter anvil/interp.py) timed on this host for a few full-size steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "anvil-lang_amd"))
+
+WORKLOAD = os.path.join(ROOT, "tests", "golden", "ir", "c2_wide_mlp.json")
+BATCH = 256
+STEPS_IN_PROGRAM = 500
+LOOP_COUNTER = "x_batch"
+PEAK_FP32_MFMA = 157.3e12
+PEAK_HBM = 8.0e12
+METRIC = "train samples/s (784-1024-1024-10 MLP, batch 256) + % of fp32-MFMA/HBM roofline"
+
+
+def load_program():
+    from anvil import irjson
+    with open(WORKLOAD) as f:
+        data = json.load(f)
+    return irjson.load(data), data
+
+
+def gpu_run(prog, data, steps: int, warmup: int):
+    from anvil.backend import hip
+    lib = hip.load(prog, seed=int(data.get("seed", 0)))
+    # timed run
+    lib.lib.anvil_marks_select(LOOP_COUNTER.encode())
+    lib.lib.anvil_sync_device()
+    t0 = time.perf_counter()
+    rc = lib.main()
+    lib.lib.anvil_sync_device()
+    wall = time.perf_counter() - t0
+    if rc != 0:
+        raise SystemExit(f"bench: the program exited with status {rc}")
+    n = lib.lib.anvil_marks_count()
+    if warmup + steps >= n:
+        raise SystemExit(f"bench: the program marks {n} iteration starts; warmup + steps must be below that")
+    ms = lib.lib.anvil_marks_elapsed_ms(warmup, warmup + steps)
+    # profiled run: per-kernel device time
+    lib.lib.anvil_marks_select(b"")
+    lib.lib.anvil_profile_enable(1)
+    lib.lib.anvil_profile_reset()
+    lib.main()
+    lib.lib.anvil_sync_device()
+    prof = lib.profile()
+    lib.lib.anvil_profile_enable(0)
+    return ms, wall, prof, lib
+
+
+def roofline(prof):
+    """The kernel with the most device time among those launched once per step."""
+    rows = [r for r in prof if r[2] >= STEPS_IN_PROGRAM]
+    label, ms, calls, flops, nbytes = max(rows, key=lambda r: r[1])
+    t = ms / calls * 1e-3
+    if flops / max(nbytes, 1) > PEAK_FP32_MFMA / PEAK_HBM:
+        achieved = flops / t / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12,
+                "unit": "TFLOP/s", "frac": round(achieved / (PEAK_FP32_MFMA / 1e12), 4), "traffic": None,
+                "kernel": label, "mean_us": round(t * 1e6, 3), "flops_per_launch": flops}
+    achieved = nbytes / t / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+            "frac": round(achieved / (PEAK_HBM / 1e9), 4), "traffic": None, "kernel": label,
+            "mean_us": round(t * 1e6, 3), "bytes_per_launch": nbytes}
+
+
+def cpu_baseline(prog, data, steps: int):
+    """The NumPy interpreter on the same IR: set-up untimed, one warm-up step, then `steps` steps."""
+    import io
+    sys.path.insert(0, ROOT)
+    from oracle import interp
+    marks = []
+
+    def hook(counter, value):
+        if counter == LOOP_COUNTER:
+            marks.append(time.perf_counter())
+            if len(marks) > steps + 1:
+                raise interp.StopRun()
+    m = interp.Machine(prog, out=io.StringIO(), seed=int(data.get("seed", 0)), loop_hook=hook)
+    try:
+        m.run()
+    except interp.StopRun:
+        pass
+    t = marks[-1] - marks[1]
+    threads = os.environ.get("OMP_NUM_THREADS") or os.environ.get("OPENBLAS_NUM_THREADS") or "unset"
+    return {"value": round(steps * BATCH / t, 2), "unit": "samples/s", "cores": 1, "kind": "port",
+            "sample": f"{steps} full-size C2 training steps (batch 256) after 1 warm-up step, NumPy "
+                      f"interpreter (oracle/interp.py), one thread of {os.cpu_count()} host CPUs "
+                      f"(OMP_NUM_THREADS={threads}); {t:.1f} s"}
+
+
+def main() -> int:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=480)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--cpu-steps", type=int, default=3)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--profile-table", action="store_true", help="print every kernel's time to stderr")
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(f"bench: this build measures one GPU only (asked for {args.gpus}); the multi-GPU design is "
+              "described in DESIGN.md and is not run", file=sys.stderr)
+        return 2
+    prog, data = load_program()
+    ms, wall, prof, lib = gpu_run(prog, data, args.steps, args.warmup)
+    if args.profile_table:
+        for label, tms, calls, flops, nbytes in sorted(prof, key=lambda r: -r[1]):
+            if calls:
+                t = tms / calls * 1e-3
+                print(f"{tms:9.3f} ms {calls:6d} x {t * 1e6:9.2f} us {flops / t / 1e12:8.3f} TFLOP/s "
+                      f"{nbytes / t / 1e9:8.1f} GB/s  {label}", file=sys.stderr)
+    value = args.steps * BATCH / (ms / 1e3)
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (generated on the device by the program: X ~ U[0,1), labels ~ U{0..9})",
+        "config": {"workload": "C2: MLP 784-1024-1024-10, ReLU, cross_entropy, adam(lr=1e-3), batch 256, "
+                               "shuffled, 500-step program", "global_batch": BATCH, "n_train": 65536,
+                   "parallelism": "single GPU", "library": os.path.basename(lib.path),
+                   "program_wall_s": round(wall, 3)},
+        "roofline": roofline(prof),
+    }
+    if not args.no_cpu:
+        cpu = cpu_baseline(prog, data, args.cpu_steps)
+        line["cpu_baseline"] = cpu
+        line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -8,6 +8,8 @@ import numpy as np
 from anvil import irjson
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ROOT_PKG = os.path.join(ROOT, "anvil-lang_amd")
 
 
 def ir_path(name):

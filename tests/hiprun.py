@@ -1,0 +1,131 @@
+"""Running generated libraries in tests, and comparing their results with the reference's.
+
+Whole programs run in a child process (`python -m anvil run`), so that a program that ends with
+a run-time error (exit status 1, as compiled Anvil programs do) ends only that child. Functions
+run in this process through the library-mode ABI (anvil.hip_function.Compiled).
+
+Comparison rules (the bar the backend is held to):
+  - printed text must be identical apart from numbers;
+  - integers (and so shuffled permutations, gathered indices, argmax results) bit for bit;
+  - a printed float within `rtol` of the reference's, or within one unit of its last printed digit;
+  - a float tensor within `rtol` of the reference's, relative to the tensor's largest magnitude.
+"""
+from __future__ import annotations
+
+import json
+import os
+import re
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+
+from fixtures import ROOT_PKG, ir_path, load_ir, vectors
+
+NUMBER = re.compile(r"[-+]?(?:\d+\.\d*|\.\d+|\d+)(?:[eE][-+]?\d+)?|[-+]?inf|nan")
+
+
+def run_program(name_or_path: str, emulate: bool, keep=(), timeout: int = 600, cwd=None, env_extra=None):
+    """(exit status, stdout, stderr, {buffer name: final contents})."""
+    path = name_or_path if name_or_path.endswith(".json") else ir_path(name_or_path)
+    with tempfile.TemporaryDirectory() as d:
+        dump = os.path.join(d, "out.npz")
+        cmd = [sys.executable, "-u", "-m", "anvil", "run", path]
+        if emulate:
+            cmd.append("--emulate")
+        if keep:
+            cmd += ["--dump", dump, "--keep", ",".join(keep)]
+        env = dict(os.environ, PYTHONPATH=ROOT_PKG + os.pathsep + os.environ.get("PYTHONPATH", ""))
+        env.update(env_extra or {})
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout, cwd=cwd or d, env=env)
+        arrays = {}
+        if keep and os.path.exists(dump):
+            z = np.load(dump)
+            arrays = {k[4:]: z[k] for k in z.files if k.startswith("buf:")}
+        return r.returncode, r.stdout, r.stderr, arrays
+
+
+def _unit(token: str) -> float:
+    """One unit of the last printed digit of a number."""
+    mant, _, exp = token.lower().partition("e")
+    dec = len(mant.split(".")[1]) if "." in mant else 0
+    return 10.0 ** (-dec) * (10.0 ** int(exp) if exp else 1.0)
+
+
+def outputs_match(want: str, got: str, rtol: float) -> str | None:
+    """None if the texts match under the rules above, else a description of the first difference."""
+    wl, gl = want.splitlines(), got.splitlines()
+    if len(wl) != len(gl):
+        return f"{len(gl)} lines, expected {len(wl)}:\n{got[-800:]}"
+    for i, (a, b) in enumerate(zip(wl, gl)):
+        if a == b:
+            continue
+        ta, tb = NUMBER.split(a), NUMBER.split(b)
+        na, nb = NUMBER.findall(a), NUMBER.findall(b)
+        if ta != tb or len(na) != len(nb):
+            return f"line {i + 1}: {b!r}, expected {a!r}"
+        for x, y in zip(na, nb):
+            fx, fy = float(x), float(y)
+            if x == y or (np.isnan(fx) and np.isnan(fy)):
+                continue
+            if abs(fx - fy) <= max(rtol * abs(fx), 1.01 * _unit(x)):
+                continue
+            return f"line {i + 1}: {y} where the reference printed {x} ({b!r})"
+    return None
+
+
+def tensors_match(want: np.ndarray, got: np.ndarray, rtol: float) -> str | None:
+    if want.shape != got.shape:
+        return f"shape {got.shape}, expected {want.shape}"
+    if want.dtype.kind in "iu":
+        bad = np.flatnonzero(want.reshape(-1) != got.reshape(-1))
+        return None if bad.size == 0 else f"{bad.size} integers differ (first at {bad[0]})"
+    scale = float(np.max(np.abs(want))) if want.size else 0.0
+    err = float(np.max(np.abs(want.astype(np.float64) - got))) if want.size else 0.0
+    if not np.isfinite(got).all() and np.isfinite(want).all():
+        return "non-finite values"
+    return None if err <= rtol * max(scale, 1e-30) else f"max |error| {err:.3g} > {rtol} x max |value| {scale:.3g}"
+
+
+def kept_buffers(name: str) -> list[str]:
+    return [k[4:] for k in vectors(name).files if k.startswith("buf:")]
+
+
+def patched_program(name: str, directory: str, **replace) -> str:
+    """A copy of a fixture's IR with strings in its run-time calls replaced (e.g. file paths)."""
+    with open(ir_path(name)) as f:
+        text = f.read()
+    for old, new in replace.items():
+        text = text.replace(old, new)
+    path = os.path.join(directory, f"{name}.json")
+    with open(path, "w") as f:
+        f.write(text)
+    return path
+
+
+def function_call(name: str, emulate: bool = False):
+    """(outputs of the generated library, golden outputs) for a function fixture."""
+    from anvil.backend import hip
+    from anvil.hip_function import Compiled, Lowered
+    prog, data = load_ir(name)
+    z = vectors(name)
+    low = Lowered.from_fixture(prog, data)
+    if emulate:
+        src = hip.generate(prog, seed=data.get("seed", 0), library=True, emulate=True)
+        lib = hip.HipLibrary(hip.compile_source(src, emulate=True), src)
+        slots = [lib.slot(b.name) for b in low.inputs]
+        args = [np.ascontiguousarray(z[f"input{k}"]) for k in range(len(low.inputs))]
+        outs = [np.empty(b.shape, np.float32 if b.dtype == "f32" else np.int32) for b in low.outputs]
+        for s, a in zip(slots, args):
+            s.value = a.ctypes.data
+        for b, o in zip(low.outputs, outs):
+            lib.slot(b.name).value = o.ctypes.data
+        lib.lib.anvil_entry()
+        got = outs
+    else:
+        fn = Compiled(low.name, low, seed=data.get("seed", 0))
+        got = fn.call([z[f"input{k}"] for k in range(len(low.inputs))])
+        got = list(got) if isinstance(got, tuple) else [got]
+    want = [z[f"output{k}"] for k in range(len(got))]
+    return got, want
