@@ -1,0 +1,262 @@
+"""Contractions on the matrix cores: recognising C = Σ_k A·B in an IR kernel and generating an
+fp32 MFMA kernel for it (the device side is hip_rt/anvil_mfma.h).
+
+A kernel qualifies when its reduction is a sum of a product of two operands, each an elementwise
+function of one load (relu(x), 0.35·k, a plain load), times constants, with loads at affine offsets
+of the loop variables alone (the reference's BLAS matcher, blas.py:113-172, finds the same shapes).
+Its variables split into
+    k: the reduction variables (in both operands), merged into one index when their strides allow;
+    m: domain variables only A uses, n: those only B uses (each merged into one row / column index);
+    batch: the rest (heads of attention, images of a convolution), one grid slice each.
+The product accumulates in the matrix cores; then every output element runs the kernel's own
+statements with acc = alpha * (the dot product): a bias add, an activation, the first moment of
+Adam, the store of a gradient — whatever the optimizer fused after the reduction. Nothing is
+split off into a second kernel.
+"""
+from __future__ import annotations
+
+from .. import ir
+from ..ir import F32, Binary, Const, Load, Unary, Var
+from . import hip_analysis as A
+from .hip_emit import Emitter, flit
+from .hip_kernels import KernelScope, Plan, decode
+
+MIN_WORK = 1 << 16           # M·N·K below which the generic schedules are as good
+CUS = 256                    # compute units of an MI355X
+
+
+def _factors(e, out):
+    if isinstance(e, Binary) and e.op == "mul" and e.dtype == F32:
+        _factors(e.a, out)
+        _factors(e.b, out)
+    else:
+        out.append(e)
+    return out
+
+
+def _const_value(e):
+    if isinstance(e, Const) and e.dtype == F32:
+        return float(e.value)
+    return None
+
+
+def _single_load(e):
+    """The one array load of an elementwise operand expression (other leaves constants), or None."""
+    loads = []
+    for x in ir.iter_expr(e):
+        if isinstance(x, Load):
+            loads.append(x)
+        elif not isinstance(x, (Const, Unary, Binary, Load)):
+            return None
+    if len(loads) != 1 or not loads[0].buf.root.shape or loads[0].buf.dtype != F32:
+        return None
+    ld = loads[0]
+    if any(not isinstance(t, Var) for t in ld.offset.terms):
+        return None
+    return ld
+
+
+def _merge(vars_, coef, coef2=None):
+    """Order vars so that their offsets form one linear index: returns (vars outer->inner, stride)
+    or None. coef2: the same vars must merge identically in a second operand."""
+    vs = sorted(vars_, key=lambda v: (abs(coef(v)), v.id))
+    if not vs:
+        return [], 0
+    base = coef(vs[0])
+    base2 = coef2(vs[0]) if coef2 else None
+    span = 1
+    for v in vs:
+        if coef(v) != base * span:
+            return None
+        if coef2 is not None and coef2(v) != base2 * span:
+            return None
+        span *= v.extent
+    return list(reversed(vs)), base
+
+
+class GemmSpec:
+    pass
+
+
+def analyse(k: ir.Kernel):
+    red = k.red
+    if red is None or red.op != "sum" or red.body.dtype != F32 or not red.vars or not k.domain:
+        return None
+    fs = _factors(red.body, [])
+    alpha = 1.0
+    ops = []
+    for f in fs:
+        c = _const_value(f)
+        if c is not None:
+            alpha *= c
+        else:
+            ops.append(f)
+    if len(ops) != 2:
+        return None
+    lds = [_single_load(e) for e in ops]
+    if None in lds:
+        return None
+    dom, rv = list(k.domain), list(red.vars)
+    best = None
+    for (ea, la), (eb, lb) in (((ops[0], lds[0]), (ops[1], lds[1])), ((ops[1], lds[1]), (ops[0], lds[0]))):
+        ca, cb = la.offset.coef, lb.offset.coef
+        if any(not ca(v) or not cb(v) for v in rv):
+            continue
+        mv = [v for v in dom if ca(v) and not cb(v)]
+        nv = [v for v in dom if cb(v) and not ca(v)]
+        bv = [v for v in dom if v not in mv and v not in nv]
+        if any(not ca(v) and not cb(v) for v in bv) or not mv or not nv:
+            continue
+        km = _merge(rv, ca, cb)
+        if km is None:
+            continue
+        mm = _merge(mv, ca)
+        if mm is None:                                   # keep the densest one as m, batch the rest
+            inner = min(mv, key=lambda v: (abs(ca(v)), v.id))
+            bv += [v for v in mv if v is not inner]
+            mm = ([inner], ca(inner))
+        nm = _merge(nv, cb)
+        if nm is None:
+            inner = min(nv, key=lambda v: (abs(cb(v)), v.id))
+            bv += [v for v in nv if v is not inner]
+            nm = ([inner], cb(inner))
+        s = GemmSpec()
+        s.k, s.alpha = k, alpha
+        s.ea, s.la, s.eb, s.lb = ea, la, eb, lb
+        s.m_vars, s.a_rs = mm
+        s.n_vars, s.b_rs = nm
+        s.k_vars, s.a_ks = km
+        s.b_ks = cb(km[0][-1]) if km[0] else 0
+        s.batch = [v for v in dom if v in bv]
+        s.M = ir.prod(v.extent for v in s.m_vars)
+        s.N = ir.prod(v.extent for v in s.n_vars)
+        s.K = ir.prod(v.extent for v in s.k_vars)
+        s.B = ir.prod(v.extent for v in s.batch)
+        # prefer the assignment whose n is the output's innermost (contiguous) variable
+        score = 1 if dom[-1] in s.n_vars else 0
+        if best is None or score > best[0]:
+            best = (score, s)
+    return None if best is None else best[1]
+
+
+def load_mode(rs, ks, T, K, const, batch_strides):
+    aligned = const % 4 == 0 and all(c % 4 == 0 for c in batch_strides)
+    if ks == 1 and K % 4 == 0 and rs % 4 == 0 and aligned:
+        return "ANVIL_LD_KC"
+    if rs == 1 and T % 4 == 0 and ks % 4 == 0 and aligned:
+        return "ANVIL_LD_RC"
+    return "ANVIL_LD_ANY"
+
+
+def match(gen, k: ir.Kernel, name: str):
+    if gen.emulate or any(st.accumulate for st in k.stores):
+        return None
+    s = analyse(k)
+    if s is None or s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < 8:
+        return None
+    return GemmPlan(gen, k, name, s)
+
+
+class GemmPlan(Plan):
+    """Schedules: "tile" (a 64 x 64 or 128 x 128 tile per workgroup, 2 x 2 wavefronts) when there are
+    enough tiles to fill the chip; else "ksplit" (a 32 x 32 tile per workgroup, K split over its four
+    wavefronts)."""
+
+    kind = "gemm"
+
+    def __init__(self, gen, k, name, spec: GemmSpec):
+        super().__init__(gen, [k], name)
+        self.k = k
+        self.s = s = spec
+        tiles = lambda bm, bn: -(-s.M // bm) * -(-s.N // bn) * s.B
+        if tiles(128, 128) >= 2 * CUS:
+            self.sched, self.BM, self.BN = "tile", 128, 128
+        elif tiles(64, 64) >= CUS:
+            self.sched, self.BM, self.BN = "tile", 64, 64
+        else:
+            self.sched, self.BM, self.BN = "ksplit", 32, 32
+        self.tm = -(-s.M // self.BM)
+        self.tn = -(-s.N // self.BN)
+        ca, cb = s.la.offset.coef, s.lb.offset.coef
+        self.amode = load_mode(s.a_rs, s.a_ks, s.M, s.K, s.la.offset.const, [ca(v) for v in s.batch])
+        self.bmode = load_mode(s.b_rs, s.b_ks, s.N, s.K, s.lb.offset.const, [cb(v) for v in s.batch])
+
+    def grid(self):
+        return (self.tn, self.tm, self.s.B), 256
+
+    def operand(self, sc, e, ld, name) -> str:
+        """A device lambda applying the operand's elementwise function to a loaded value."""
+        if e is ld:
+            return f"    anvil_identity_op {name};"
+        lines: list[str] = []
+        em = Emitter(sc, lines, "        ", prefix=f"{name}_")
+        saved = sc.fwd, sc.canon
+        sc.canon = {v: ("v", v.id) for v in ld.offset.terms}
+        sc.fwd = {_key(ld): "x"}
+        v = em.ex(e)
+        sc.fwd, sc.canon = saved
+        return "\n".join([f"    auto {name} = [=](float x) -> float {{"] + lines + [f"        return {v};", "    };"])
+
+    def source(self) -> str:
+        s, k = self.s, self.k
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(k)
+        a_ptr = sc.buf(s.la.buf)
+        b_ptr = sc.buf(s.lb.buf)
+        body = [self.operand(sc, s.ea, s.la, "opa"), self.operand(sc, s.eb, s.lb, "opb"),
+                f"    const int m0 = blockIdx.y * {self.BM}, n0 = blockIdx.x * {self.BN};",
+                "    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;"]
+        ca, cb = s.la.offset.coef, s.lb.offset.coef
+        a_off = [str(s.la.offset.const)]
+        b_off = [str(s.lb.offset.const)]
+        if s.batch:
+            body += ["    " + line for line in decode(s.batch, "blockIdx.z", "uint32_t")]
+            for v in s.batch:
+                if ca(v):
+                    a_off.append(f"{ca(v)}LL * v{v.id}")
+                if cb(v):
+                    b_off.append(f"{cb(v)}LL * v{v.id}")
+        body.append(f"    const float *pa = {a_ptr} + ({' + '.join(a_off)});")
+        body.append(f"    const float *pb = {b_ptr} + ({' + '.join(b_off)});")
+        args = f"pa, {s.a_rs}LL, {s.a_ks}LL, pb, {s.b_rs}LL, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, 0, {s.K}, opa, opb"
+        if self.sched == "tile":
+            tm, tn = self.BM // 64, self.BN // 64
+            body += [f"    anvil_mm_acc<{tm}, {tn}> acc;",
+                     f"    anvil_mm_tile<{self.BM}, {self.BN}, {self.amode}, {self.bmode}>(acc, {args});",
+                     f"    const int wm = (wave >> 1) * {self.BM // 2}, wn = (wave & 1) * {self.BN // 2};",
+                     "#pragma unroll", f"    for (int ti = 0; ti < {tm}; ti++)",
+                     "#pragma unroll", f"    for (int tj = 0; tj < {tn}; tj++)",
+                     "#pragma unroll", "    for (int vv = 0; vv < 16; vv++) {",
+                     "        const int mi = m0 + wm + 32 * ti + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
+                     "        const int ni = n0 + wn + 32 * tj + (lane & 31);",
+                     f"        if (mi >= {s.M} || ni >= {s.N}) continue;",
+                     f"        const float acc_v = {flit(s.alpha)} * acc.c[ti][tj][vv];"]
+        else:
+            body += ["    float part[1][1][4];",
+                     f"    anvil_mm_tile_ksplit<1, 1, {self.amode}, {self.bmode}>(part, {args});",
+                     "#pragma unroll", "    for (int q = 0; q < 4; q++) {",
+                     "        const int mi = m0 + 8 * wave + 4 * (lane >> 5) + q;",
+                     "        const int ni = n0 + (lane & 31);",
+                     f"        if (mi >= {s.M} || ni >= {s.N}) continue;",
+                     f"        const float acc_v = {flit(s.alpha)} * part[0][0][q];"]
+        lines: list[str] = []
+        em = Emitter(sc, lines, "        ")
+        for line in decode(s.m_vars, "(uint32_t)mi", "uint32_t"):
+            em.emit(line)
+        for line in decode(s.n_vars, "(uint32_t)ni", "uint32_t"):
+            em.emit(line)
+        strides = ir.row_major_strides([v.extent for v in k.domain])
+        sc.rand = " + ".join(f"{st}u * (uint32_t)v{v.id}" for v, st in zip(k.domain, strides)) or "0u"
+        sc.acc_name = "acc_v"
+        self.statements(em, k, sc, parallel=True)
+        body += lines
+        body += ["    }", "}"]
+        head = [self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
+                + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, B {self.bmode[9:]}",
+                self.header(256) + " {"]
+        return "\n".join(head + body)
+
+
+def _key(ld):
+    from .hip_kernels import canon_key
+    return canon_key(ld.buf, ld.offset, {v: ("v", v.id) for v in ld.offset.terms})
