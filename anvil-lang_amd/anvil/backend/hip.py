@@ -193,7 +193,7 @@ class HipGen:
         if self.gemm is not None:
             g = self.gemm.match(self, k, name)
             if g is not None:
-                return g, 1
+                return g, 1 + self.absorb_followers(g, stmts, i + 1)
         ty = HK.split_ways(k, self.emulate)
         if ty > 1:
             return HK.SplitPlan(self, k, name, ty), 1
@@ -208,6 +208,35 @@ class HipGen:
         self.mark_dead_stores(plan)
         return plan, j - i
 
+    def absorb_followers(self, plan, stmts, j) -> int:
+        """Elementwise kernels right after a product (past host-only scalar kernels, which are then
+        computed before the launch) that can run in its epilogue; returns the statements taken."""
+        taken = 0
+        hoist = []
+        k = plan.kernels[0]
+        reads_k = {b.id for b in A.kernel_reads(k)}
+        while j + taken < len(stmts) and isinstance(stmts[j + taken], KernelStmt):
+            e = stmts[j + taken].kernel
+            if A.is_host_kernel(e, self.hosts):
+                if {st.buf.root.id for st in e.stores} & reads_k:
+                    break
+                hoist.append(e)
+                taken += 1
+                continue
+            how = self.gemm.follower(k, e, self.hosts)
+            if how is None:
+                break
+            plan.absorb(e, how)
+            taken += 1
+            plan.hoisted = list(getattr(plan, "hoisted", [])) + hoist
+            hoist = []
+            if len(plan.kernels) >= 3:
+                break
+        taken -= len(hoist)                             # host kernels after the last follower stay put
+        if len(plan.kernels) > 1:
+            self.mark_dead_stores(plan)
+        return taken
+
     def mark_dead_stores(self, plan):
         """Stores of a row group whose buffer only the group reads (from registers) are dropped."""
         if len(plan.kernels) < 2:
@@ -216,6 +245,18 @@ class HipGen:
         for k in plan.kernels:
             for b in A.kernel_reads(k):
                 readers_in[b.id] = readers_in.get(b.id, 0) + 1
+        if plan.kind == "gemm":
+            k = plan.kernels[0]
+            for i, st in enumerate(k.stmts):
+                if not isinstance(st, ir.Store):
+                    continue
+                b = st.buf.root
+                if b.kind not in A.SHARED_KINDS or self.is_host(b) or getattr(b, "heap", False):
+                    continue
+                # dead: the product itself does not read it, and only its followers (from registers) do
+                if b not in A.kernel_reads(k) and self.readers.get(b.id, 0) == readers_in.get(b.id, 0):
+                    plan.skip_stores.add((k.id, i))
+            return
         for k in plan.kernels:
             cm = plan.canon_map(k)
             _, inner = plan.stage_vars(k)
@@ -255,6 +296,8 @@ class HipGen:
                         self.group_of[kk.id] = plan
                 else:
                     plan, used = plan
+                for hk in getattr(plan, "hoisted", []):
+                    out += self.host_kernel(hk, ind)
                 out += self.launch(plan, ind)
                 i += used
                 continue

@@ -15,13 +15,16 @@ split off into a second kernel.
 """
 from __future__ import annotations
 
+import os
+
 from .. import ir
 from ..ir import F32, Binary, Const, Load, Unary, Var
 from . import hip_analysis as A
 from .hip_emit import Emitter, flit
-from .hip_kernels import KernelScope, Plan, decode
+from .hip_kernels import KernelScope, Plan, canon_key, decode
 
 MIN_WORK = 1 << 16           # M·N·K below which the generic schedules are as good
+MIN_SIDE = 32                # a narrower product (10 classes) wastes most of a 32-wide MFMA tile
 CUS = 256                    # compute units of an MI355X
 
 
@@ -152,9 +155,68 @@ def match(gen, k: ir.Kernel, name: str):
     if gen.emulate or any(st.accumulate for st in k.stores):
         return None
     s = analyse(k)
-    if s is None or s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < 8:
+    if s is None or s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < MIN_SIDE:
         return None
     return GemmPlan(gen, k, name, s)
+
+
+def subst_affine(a: ir.Affine, m: dict):
+    """a with its loop variables replaced by affine expressions (None if a has gathers)."""
+    out = ir.Affine(a.const)
+    for t, c in a.terms.items():
+        if isinstance(t, Var):
+            if t not in m:
+                return None
+            out = out + m[t] * c
+        elif isinstance(t, ir.ScalarRef):
+            out = out + ir.Affine(0, {t: c})
+        else:
+            return None
+    return out
+
+
+def follower_map(k: ir.Kernel, e: ir.Kernel):
+    """e's domain variables as affine functions of k's, when e walks k's output elements in the same
+    row-major order (the same shape, or one flattened variable)."""
+    ke, ee = [v.extent for v in k.domain], [v.extent for v in e.domain]
+    if ir.prod(ke) != ir.prod(ee) or not ee:
+        return None
+    if ke == ee:
+        return {ev: ir.Affine.of(kv) for ev, kv in zip(e.domain, k.domain)}
+    if len(e.domain) == 1:
+        flat = ir.Affine(0)
+        for kv, st in zip(k.domain, ir.row_major_strides(ke)):
+            flat = flat + ir.Affine(0, {kv: st})
+        return {e.domain[0]: flat}
+    return None
+
+
+def follower(k: ir.Kernel, e: ir.Kernel, hosts: set):
+    """(var map, forwarded loads) if elementwise kernel e can run in k's epilogue, element by element:
+    every load e makes of what k writes is of the element k just wrote there (so the value comes
+    from a register), and k reads nothing that e writes."""
+    if (e.red is not None or e.uses_rand() or A.is_host_kernel(e, hosts) or not A.parallel_safe(e)
+            or any(st.accumulate for st in e.stores)):
+        return None
+    m = follower_map(k, e)
+    if m is None:
+        return None
+    stored = {}
+    for st in k.stores:
+        if st.buf.root.id in stored:
+            return None
+        stored[st.buf.root.id] = st.offset
+    fwd = []
+    for ld in A.kernel_loads(e):
+        bid = ld.buf.root.id
+        if bid in stored:
+            sub = subst_affine(ld.offset, m)
+            if sub is None or sub != stored[bid]:
+                return None
+            fwd.append(ld)
+    if {b.id for b in A.kernel_writes(e)} & {b.id for b in A.kernel_reads(k)}:
+        return None
+    return m, fwd
 
 
 class GemmPlan(Plan):
@@ -171,18 +233,61 @@ class GemmPlan(Plan):
         tiles = lambda bm, bn: -(-s.M // bm) * -(-s.N // bn) * s.B
         if tiles(128, 128) >= 2 * CUS:
             self.sched, self.BM, self.BN = "tile", 128, 128
-        elif tiles(64, 64) >= CUS:
+        elif tiles(64, 64) >= 4 * CUS:
             self.sched, self.BM, self.BN = "tile", 64, 64
         else:
             self.sched, self.BM, self.BN = "ksplit", 32, 32
+        # the K split: enough wavefronts that each one's share (a few 8-k chunks) is in flight at once
+        self.waves = 16 if s.K >= 512 else (8 if s.K >= 128 else 4)
+        self.unroll = 4
+        force = os.environ.get("ANVIL_GEMM_FORCE")       # tuning: "tile64" | "tile128" | "ksplit:W:U"
+        if force:
+            parts = force.split(":")
+            if parts[0].startswith("tile"):
+                self.sched, self.BM = "tile", int(parts[0][4:])
+                self.BN = self.BM
+            else:
+                self.sched, self.BM, self.BN = "ksplit", 32, 32
+                self.waves, self.unroll = int(parts[1]), int(parts[2])
+        self.threads = 64 * self.waves if self.sched == "ksplit" else 256
         self.tm = -(-s.M // self.BM)
         self.tn = -(-s.N // self.BN)
         ca, cb = s.la.offset.coef, s.lb.offset.coef
         self.amode = load_mode(s.a_rs, s.a_ks, s.M, s.K, s.la.offset.const, [ca(v) for v in s.batch])
         self.bmode = load_mode(s.b_rs, s.b_ks, s.N, s.K, s.lb.offset.const, [cb(v) for v in s.batch])
+        self.followers = []             # (kernel, var map, forwarded loads) run in the epilogue
+
+    def hoistable(self, stages):
+        """(stage, load) pairs of the epilogue that may be issued before the K loop: plain loads of
+        buffers no earlier epilogue statement stores to (later statements must see those stores)."""
+        stored: set = set()
+        out, seen = [], set()
+        for si, (e, m, fwd) in enumerate(stages):
+            fwd_ids = {id(ld) for ld in fwd}
+            canon = {v: ("e", v.id) for v in e.domain}
+            for st in e.stmts:
+                for ld in ir.loads_in(st.value):
+                    b = ld.buf.root
+                    if id(ld) in fwd_ids or not b.shape or b.id in stored or ld.offset.gathers():
+                        continue
+                    if any(isinstance(t, ir.ScalarRef) for t in ld.offset.terms):
+                        continue
+                    key = (si, canon_key(ld.buf, ld.offset, canon))
+                    if key not in seen:
+                        seen.add(key)
+                        out.append((si, ld))
+                if isinstance(st, ir.Store):
+                    stored.add(st.buf.root.id)
+        return out
+
+    def absorb(self, e, how):
+        m, fwd = how
+        self.followers.append((e, m, fwd))
+        self.kernels.append(e)
+        self.label += " + " + (e.label or e.name)
 
     def grid(self):
-        return (self.tn, self.tm, self.s.B), 256
+        return (self.tn, self.tm, self.s.B), self.threads
 
     def operand(self, sc, e, ld, name) -> str:
         """A device lambda applying the operand's elementwise function to a loaded value."""
@@ -221,39 +326,79 @@ class GemmPlan(Plan):
         args = f"pa, {s.a_rs}LL, {s.a_ks}LL, pb, {s.b_rs}LL, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, 0, {s.K}, opa, opb"
         if self.sched == "tile":
             tm, tn = self.BM // 64, self.BN // 64
-            body += [f"    anvil_mm_acc<{tm}, {tn}> acc;",
-                     f"    anvil_mm_tile<{self.BM}, {self.BN}, {self.amode}, {self.bmode}>(acc, {args});",
-                     f"    const int wm = (wave >> 1) * {self.BM // 2}, wn = (wave & 1) * {self.BN // 2};",
-                     "#pragma unroll", f"    for (int ti = 0; ti < {tm}; ti++)",
-                     "#pragma unroll", f"    for (int tj = 0; tj < {tn}; tj++)",
-                     "#pragma unroll", "    for (int vv = 0; vv < 16; vv++) {",
-                     "        const int mi = m0 + wm + 32 * ti + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
-                     "        const int ni = n0 + wn + 32 * tj + (lane & 31);",
-                     f"        if (mi >= {s.M} || ni >= {s.N}) continue;",
-                     f"        const float acc_v = {flit(s.alpha)} * acc.c[ti][tj][vv];"]
+            per = tm * tn * 16
+            loop = ["#pragma unroll", f"    for (int ti = 0; ti < {tm}; ti++)",
+                    "#pragma unroll", f"    for (int tj = 0; tj < {tn}; tj++)",
+                    "#pragma unroll", "    for (int vv = 0; vv < 16; vv++) {",
+                    "        const int mi = m0 + wm + 32 * ti + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
+                    "        const int ni = n0 + wn + 32 * tj + (lane & 31);",
+                    f"        if (mi >= {s.M} || ni >= {s.N}) continue;"]
+            slot = f"(ti * {tn} + tj) * 16 + vv"
+            body.append(f"    const int wm = (wave >> 1) * {self.BM // 2}, wn = (wave & 1) * {self.BN // 2};")
+            main = [f"    anvil_mm_acc<{tm}, {tn}> acc;",
+                    f"    anvil_mm_tile<{self.BM}, {self.BN}, {self.amode}, {self.bmode}>(acc, {args});"]
+            value = "acc.c[ti][tj][vv]"
         else:
-            body += ["    float part[1][1][4];",
-                     f"    anvil_mm_tile_ksplit<1, 1, {self.amode}, {self.bmode}>(part, {args});",
-                     "#pragma unroll", "    for (int q = 0; q < 4; q++) {",
-                     "        const int mi = m0 + 8 * wave + 4 * (lane >> 5) + q;",
-                     "        const int ni = n0 + (lane & 31);",
-                     f"        if (mi >= {s.M} || ni >= {s.N}) continue;",
-                     f"        const float acc_v = {flit(s.alpha)} * part[0][0][q];"]
+            W = self.waves
+            per = 16 // W
+            loop = ["#pragma unroll", f"    for (int q = 0; q < {per}; q++) {{",
+                    f"        const int vv = {per} * wave + q;",
+                    "        const int mi = m0 + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
+                    "        const int ni = n0 + (lane & 31);",
+                    f"        if (mi >= {s.M} || ni >= {s.N}) continue;"]
+            slot = "q"
+            main = [f"    float part[1][1][{per}];",
+                    f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]
+            value = "part[0][0][q]"
+        stages = [(k, None, [])] + list(self.followers)
+        hoisted = self.hoistable(stages) if per * 4 <= 64 else []
+        hoisted = hoisted[:max(0, 64 // per)]
+
+        def element_vars(em):
+            for line in decode(s.m_vars, "(uint32_t)mi", "uint32_t"):
+                em.emit(line)
+            for line in decode(s.n_vars, "(uint32_t)ni", "uint32_t"):
+                em.emit(line)
+            for e, m, _ in self.followers:
+                for ev, aff in m.items():
+                    em.emit(f"const int v{ev.id} = (int)({em.affine(aff)});")
+        # epilogue operands that do not depend on the product are loaded before the K loop
+        if hoisted:
+            body.append("    " + " ".join(f"float pre{i}[{per}];" for i in range(len(hoisted))))
+            body += loop
+            pl: list[str] = []
+            pem = Emitter(sc, pl, "        ", prefix="p")
+            element_vars(pem)
+            for i, (si, ld) in enumerate(hoisted):
+                pem.emit(f"pre{i}[{slot}] = {pem.build(ld)};")
+            body += pl + ["    }"]
+        body += main
+        body += loop + [f"        const float acc_v = {flit(s.alpha)} * {value};"]
         lines: list[str] = []
         em = Emitter(sc, lines, "        ")
-        for line in decode(s.m_vars, "(uint32_t)mi", "uint32_t"):
-            em.emit(line)
-        for line in decode(s.n_vars, "(uint32_t)ni", "uint32_t"):
-            em.emit(line)
+        element_vars(em)
         strides = ir.row_major_strides([v.extent for v in k.domain])
         sc.rand = " + ".join(f"{st}u * (uint32_t)v{v.id}" for v, st in zip(k.domain, strides)) or "0u"
         sc.acc_name = "acc_v"
-        self.statements(em, k, sc, parallel=True)
+        stored = {}
+
+        def on_store(st, val):
+            stored[st.buf.root.id] = val
+        for si, (e, m, fwd) in enumerate(stages):
+            em.reset_memo()
+            canon = {v: ("e", v.id) for v in e.domain}
+            sc.canon = canon
+            sc.fwd = {canon_key(ld.buf, ld.offset, canon): stored[ld.buf.root.id] for ld in fwd}
+            for i, (sj, ld) in enumerate(hoisted):
+                if sj == si:
+                    sc.fwd[canon_key(ld.buf, ld.offset, canon)] = f"pre{i}[{slot}]"
+            self.statements(em, e, sc, parallel=True, on_store=on_store)
+        sc.canon, sc.fwd = None, {}
         body += lines
         body += ["    }", "}"]
         head = [self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
                 + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, B {self.bmode[9:]}",
-                self.header(256) + " {"]
+                self.header(self.threads) + " {"]
         return "\n".join(head + body)
 
 

@@ -169,69 +169,79 @@ __device__ __forceinline__ void anvil_mm_tile(anvil_mm_acc<BM / 64, BN / 64> &ac
     }
 }
 
-// K split inside one workgroup: the 4 wavefronts all compute the same (32 TM) x (32 TN) tile, wave w
-// over the 16-deep k slices w, w + 4, w + 8, ... (every wave runs the same number of rounds; a
-// slice past the end loads zeros). Each wave stages its own slices in its own LDS region. At the
-// end the four partial tiles are added through LDS in wave order (a fixed order: the result does
-// not depend on timing) and wave w keeps accumulators 4w .. 4w+3 of every 32x32 sub-tile in `out`.
-template <int TM, int TN, int AMODE, int BMODE, class OPA, class OPB>
-__device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][4],
+// K split inside one workgroup: its W wavefronts all compute the same (32 TM) x (32 TN) tile, wave w
+// over the w-th of W equal shares of K. The waves share no operands, so each loads its MFMA operands straight
+// from global memory into registers, U chunks of 8 k at a time, one batch ahead of the MFMAs: lane
+// l (row or column r = l % 32, half h = l / 32) holds element k0 + 4h + s of its row of A and of its
+// column of B for s = 0..3, and MFMA s of the chunk takes slot s (any assignment of k values to
+// MFMA k slots gives the same sum, as long as A and B agree). A k-contiguous operand is one float4
+// per lane and chunk; otherwise 4 loads, coalesced across the 32 lanes when the row index is
+// contiguous. At the end the W partial tiles are added through LDS in wave order (a fixed order:
+// the result does not depend on timing) and wave w keeps accumulators (16/W) w .. (16/W)(w+1) - 1
+// of every 32x32 sub-tile in `out`.
+template <int MODE, class OP>
+__device__ __forceinline__ void anvil_chunk_load(float (&r)[4], const float *__restrict__ p, long long rs, long long ks,
+                                                 int t, int tmax, int k, int kend, OP op) {
+    if (MODE == ANVIL_LD_KC) {
+        anvil_f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (t < tmax && k < kend) v = *(const anvil_f32x4 *)(p + (long long)t * rs + k);
+        r[0] = (t < tmax && k + 0 < kend) ? op(v.x) : 0.f;
+        r[1] = (t < tmax && k + 1 < kend) ? op(v.y) : 0.f;
+        r[2] = (t < tmax && k + 2 < kend) ? op(v.z) : 0.f;
+        r[3] = (t < tmax && k + 3 < kend) ? op(v.w) : 0.f;
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+            r[s] = (t < tmax && k + s < kend) ? op(p[(long long)t * rs + (long long)(k + s) * ks]) : 0.f;
+    }
+}
+
+template <int TM, int TN, int AMODE, int BMODE, int U, class OPA, class OPB>
+__device__ __forceinline__ void anvil_mm_wave(anvil_mm_acc<TM, TN> &acc,
+                                              const float *__restrict__ a, long long a_rs, long long a_ks,
+                                              const float *__restrict__ b, long long b_rs, long long b_ks,
+                                              int M, int N, int m0, int n0, int kbeg, int kend, OPA opa, OPB opb) {
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    float a0[U][TM][4], b0[U][TN][4], a1[U][TM][4], b1[U][TN][4];
+    constexpr int STEP = 8 * U;
+    acc.zero();
+#define ANVIL_MM_LOAD(AR, BR, KB)                                                                          \
+    _Pragma("unroll") for (int u = 0; u < U; u++) {                                                        \
+        _Pragma("unroll") for (int i = 0; i < TM; i++)                                                     \
+            anvil_chunk_load<AMODE>(AR[u][i], a, a_rs, a_ks, m0 + 32 * i + r, M, (KB) + 8 * u + 4 * h, kend, opa); \
+        _Pragma("unroll") for (int j = 0; j < TN; j++)                                                     \
+            anvil_chunk_load<BMODE>(BR[u][j], b, b_rs, b_ks, n0 + 32 * j + r, N, (KB) + 8 * u + 4 * h, kend, opb); \
+    }
+#define ANVIL_MM_MFMA(AR, BR)                                                                              \
+    _Pragma("unroll") for (int u = 0; u < U; u++)                                                          \
+        _Pragma("unroll") for (int s = 0; s < 4; s++)                                                      \
+            _Pragma("unroll") for (int i = 0; i < TM; i++)                                                 \
+                _Pragma("unroll") for (int j = 0; j < TN; j++)                                             \
+                    acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(AR[u][i][s], BR[u][j][s], acc.c[i][j], 0, 0, 0);
+    ANVIL_MM_LOAD(a0, b0, kbeg)
+    for (int kb = kbeg; kb < kend; kb += 2 * STEP) {
+        ANVIL_MM_LOAD(a1, b1, kb + STEP)
+        ANVIL_MM_MFMA(a0, b0)
+        if (kb + STEP >= kend) break;                  // the second batch is past the end: all zeros
+        ANVIL_MM_LOAD(a0, b0, kb + 2 * STEP)
+        ANVIL_MM_MFMA(a1, b1)
+    }
+#undef ANVIL_MM_LOAD
+#undef ANVIL_MM_MFMA
+}
+
+template <int W, int TM, int TN, int AMODE, int BMODE, int U, class OPA, class OPB>
+__device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][16 / W],
                                                      const float *__restrict__ a, long long a_rs, long long a_ks,
                                                      const float *__restrict__ b, long long b_rs, long long b_ks,
                                                      int M, int N, int m0, int n0, int kbeg, int kend, OPA opa, OPB opb) {
-    constexpr int BM = 32 * TM, BN = 32 * TN;
-    constexpr int SA = ANVIL_MM_BK * (BM + 4), SB = ANVIL_MM_BK * (BN + 4);
-    static_assert(4 * TM * TN * 16 * 64 <= 4 * 2 * (SA + SB), "partial tiles must fit in the staging LDS");
-    __shared__ float lds[4 * 2 * (SA + SB)];
+    constexpr int PER = 16 / W;                                       // accumulators each wave finishes
+    __shared__ float part[W * TM * TN * 16 * 64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int lr = lane & 31, lk = lane >> 5;
-    float *As = lds + w * 2 * (SA + SB);
-    float *Bs = As + 2 * SA;
-    anvil_slice<BM, AMODE, 64> sa;
-    anvil_slice<BN, BMODE, 64> sb;
+    const int share = ((kend - kbeg + W - 1) / W + 7) / 8 * 8;        // a multiple of the 8-k chunk
+    const int kb = kbeg + w * share, ke = min(kend, kb + share);
     anvil_mm_acc<TM, TN> acc;
-    acc.zero();
-    const int slices = (kend - kbeg + ANVIL_MM_BK - 1) / ANVIL_MM_BK;
-    const int rounds = (slices + 3) / 4;
-    int k0 = kbeg + ANVIL_MM_BK * w;
-    sa.load(a, a_rs, a_ks, m0, M, k0, kend, opa, lane);
-    sb.load(b, b_rs, b_ks, n0, N, k0, kend, opb, lane);
-    sa.store(As, lane);
-    sb.store(Bs, lane);
-    __syncthreads();
-    int buf = 0;
-    for (int r = 0; r < rounds; r++) {
-        const int kn = k0 + 4 * ANVIL_MM_BK;
-        const bool more = r + 1 < rounds;
-        if (more) {
-            sa.load(a, a_rs, a_ks, m0, M, kn, kend, opa, lane);
-            sb.load(b, b_rs, b_ks, n0, N, kn, kend, opb, lane);
-        }
-        const float *as = As + buf * SA;
-        const float *bs = Bs + buf * SB;
-#pragma unroll
-        for (int kk = 0; kk < ANVIL_MM_BK; kk += 2) {
-            float fa[TM], fb[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++) fa[i] = as[(kk + lk) * (BM + 4) + 32 * i + lr];
-#pragma unroll
-            for (int j = 0; j < TN; j++) fb[j] = bs[(kk + lk) * (BN + 4) + 32 * j + lr];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc.c[i][j], 0, 0, 0);
-        }
-        if (more) {
-            sa.store(As + (buf ^ 1) * SA, lane);
-            sb.store(Bs + (buf ^ 1) * SB, lane);
-        }
-        __syncthreads();
-        buf ^= 1;
-        k0 = kn;
-    }
-    // the four partial tiles, through LDS (the staging area is free now): part[w][i][j][v][lane]
-    float *part = lds;
+    anvil_mm_wave<TM, TN, AMODE, BMODE, U>(acc, a, a_rs, a_ks, b, b_rs, b_ks, M, N, m0, n0, kb, ke, opa, opb);
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -244,10 +254,10 @@ __device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][4],
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
+            for (int q = 0; q < PER; q++) {
                 float s = 0.f;
 #pragma unroll
-                for (int src = 0; src < 4; src++) s += part[(((src * TM + i) * TN + j) * 16 + 4 * w + q) * 64 + lane];
+                for (int src = 0; src < W; src++) s += part[(((src * TM + i) * TN + j) * 16 + PER * w + q) * 64 + lane];
                 out[i][j][q] = s;
             }
 }
