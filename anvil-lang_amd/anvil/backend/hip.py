@@ -104,13 +104,19 @@ class HostScope(Scope):
 # ----------------------------------------------------------------------------- the generator
 
 class HipGen:
-    def __init__(self, prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False):
+    def __init__(self, prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False,
+                 graphs: bool = False):
         self.prog = prog
         self.seed = seed & 0xFFFFFFFF
         self.library = library
         self.emulate = emulate
         self.hosts = A.host_scalars(prog)
         self.readers = A.all_readers(prog)
+        self.graphs = graphs
+        self.dev_hosts = self.device_visible_hosts() if graphs else set()
+        self.hsd = {bid: i for i, bid in enumerate(sorted(self.dev_hosts))}
+        self.twins: dict = {}             # host kernel id -> its device twin plan
+        self.segments: list = []          # C functions of graph segments
         self.by_id = {b.root.id: b.root for b in prog.buffers}
         self.faults: list[str] = []
         self.tables: list[str] = []
@@ -128,6 +134,43 @@ class HipGen:
                 self.gemm = hip_gemm
             except ImportError:
                 self.gemm = None
+
+    def device_visible_hosts(self) -> set:
+        """Host scalars kernels read, and (closing over the host's scalar kernels that compute
+        them) everything those are computed from: the device keeps its own copy of these."""
+        out: set = set()
+        host_ks = []
+        for k in ir.all_kernels(self.prog):
+            if A.is_host_kernel(k, self.hosts):
+                host_ks.append(k)
+            else:
+                out |= {b.id for b in A.kernel_reads(k) if b.id in self.hosts}
+        grown = True
+        while grown:
+            grown = False
+            for k in host_ks:
+                if {st.buf.root.id for st in k.stores} & out:
+                    more = {b.id for b in A.kernel_reads(k) if b.id in self.hosts} - out
+                    if more:
+                        out |= more
+                        grown = True
+        return out
+
+    def hsd_slot(self, b) -> int:
+        r = b.root
+        if r.id not in self.hsd:
+            raise AssertionError(f"host scalar {r.name} is read on the device but has no device copy")
+        return self.hsd[r.id]
+
+    def twin_of(self, k):
+        """The device twin of a host kernel that computes device-visible scalars, or None."""
+        if not self.graphs or not ({st.buf.root.id for st in k.stores} & self.dev_hosts):
+            return None
+        t = self.twins.get(k.id)
+        if t is None:
+            t = self.twins[k.id] = HK.TwinPlan(self, k, f"tw{k.id}")
+            self.plans.append(t)
+        return t
 
     # ------------------------------------------------------------------ small helpers
     def fault(self, message: str) -> int:
@@ -193,6 +236,8 @@ class HipGen:
         if self.gemm is not None:
             g = self.gemm.match(self, k, name)
             if g is not None:
+                if os.environ.get("ANVIL_GEMM_FUSE", "1") == "0":      # tuning: no epilogue fusion
+                    return g, 1
                 return g, 1 + self.absorb_followers(g, stmts, i + 1)
         ty = HK.split_ways(k, self.emulate)
         if ty > 1:
@@ -275,16 +320,41 @@ class HipGen:
                 plan.skip_stores.add((k.id, i))
 
     # ------------------------------------------------------------------ host code
-    def block(self, blk: ir.Block, ind: str) -> list[str]:
+    def block(self, blk: ir.Block, ind: str, in_loop: bool = False, tail=None) -> list[str]:
+        """Host code of a block. In a loop body, each straight run of kernels (device launches and
+        the host's scalar kernels) becomes a graph segment. `tail`: launch lines to run at the end
+        of the block (a loop counter's twin), put inside the last segment when it ends the block;
+        self.tail_used says whether that happened."""
         out = []
+        seg: list = []                  # (kind, lines, plan) of the pending run
         stmts = blk.stmts
+        self.tail_used = False
+
+        def flush(last: bool):
+            if not seg:
+                return
+            if last and tail is not None and in_loop and self.graphs:
+                seg.append(("twin", tail, None))
+                self.tail_used = True
+            launches = sum(1 for kind, _, _ in seg if kind != "host")
+            rand = any(p is not None and p.streams for _, _, p in seg)
+            if in_loop and self.graphs and launches >= 2 and not rand:
+                out.extend(self.segment(seg, ind))
+            else:
+                for _, lines, _ in seg:
+                    out.extend(lines)
+            seg.clear()
+
         i = 0
         while i < len(stmts):
             st = stmts[i]
             if isinstance(st, KernelStmt):
                 k = st.kernel
                 if A.is_host_kernel(k, self.hosts):
-                    out += self.host_kernel(k, ind)
+                    seg.append(("host", self.host_kernel(k, ind), None))
+                    twin = self.twin_of(k)
+                    if twin is not None:
+                        seg.append(("twin", self.launch(twin, ind), twin))
                     i += 1
                     continue
                 plan = self.plan_of.get(k.id)
@@ -297,13 +367,36 @@ class HipGen:
                 else:
                     plan, used = plan
                 for hk in getattr(plan, "hoisted", []):
-                    out += self.host_kernel(hk, ind)
-                out += self.launch(plan, ind)
+                    seg.append(("host", self.host_kernel(hk, ind), None))
+                    twin = self.twin_of(hk)
+                    if twin is not None:
+                        seg.append(("twin", self.launch(twin, ind), twin))
+                seg.append(("launch", self.launch(plan, ind), plan))
                 i += used
                 continue
+            flush(False)
             out += self.stmt(st, ind)
             i += 1
+        flush(True)
+        if tail is not None and not self.tail_used:
+            out.extend(tail)
+            self.tail_used = True
         return out
+
+    def segment(self, seg: list, ind: str) -> list[str]:
+        """A graph segment: a function that records the run (host kernels, twins, launches) and one
+        that does only the host's part, for replays."""
+        n = len(self.segments)
+        rec = [f"static void anvil_seg{n}_record(void) {{"]
+        host = [f"static void anvil_seg{n}_host(void) {{"]
+        for kind, lines, _ in seg:
+            rec.extend(lines)
+            if kind == "host":
+                host.extend(lines)
+            else:
+                host.extend(line for line in lines if line.startswith("@@dirty "))
+        self.segments.append(rec + ["}"] + host + ["}"])
+        return [f"{ind}anvil_segment_run(&anvil_seg{n}, anvil_seg{n}_record, anvil_seg{n}_host);"]
 
     def host_kernel(self, k: ir.Kernel, ind: str) -> list[str]:
         lines = [f"{ind}{{   // {k.name}: on the host"]
@@ -345,9 +438,9 @@ class HipGen:
         if isinstance(st, ir.For):
             return self.for_(st, ind)
         if isinstance(st, ir.While):
-            out = [f"{ind}while (1) {{"] + self.block(st.cond_block, ind + "    ")
+            out = [f"{ind}while (1) {{"] + self.block(st.cond_block, ind + "    ", in_loop=True)
             out.append(f"{ind}    if ({self.scalar_value(st.cond)} == 0) break;")
-            return out + self.block(st.body, ind + "    ") + [f"{ind}}}"]
+            return out + self.block(st.body, ind + "    ", in_loop=True) + [f"{ind}}}"]
         if isinstance(st, ir.If):
             out = [f"{ind}if ({self.scalar_value(st.cond)} != 0) {{"] + self.block(st.then, ind + "    ")
             if st.orelse.stmts:
@@ -378,9 +471,19 @@ class HipGen:
         name = c_string(c.name)
         out = [f"{ind}{{", f"{ind}    const long long stop_ = {stop};"]
         if self.is_host(c):
-            out.append(f"{ind}    for (anvil_h{c.id} = (int)({start}); anvil_h{c.id} < stop_; anvil_h{c.id} += {st.step}) {{")
+            tail = None
+            step_twin = ""
+            if c.id in self.dev_hosts:
+                slot = self.hsd_slot(c)
+                out.append(f"{ind}    ANVIL_GO(anvil_twin_set, 1, 64, anvil_hsd, {slot}, (int)({start}));")
+                tail = [f"{ind}        ANVIL_GO(anvil_twin_step, 1, 64, anvil_hsd, {slot}, {st.step});"]
+                body_has_continue = any(isinstance(x, ir.Continue) for b in ir.walk_blocks(st.body) for x in b.stmts)
+                if body_has_continue:
+                    step_twin = f"ANVIL_GO(anvil_twin_step, 1, 64, anvil_hsd, {slot}, {st.step}), "
+                    tail = None
+            out.append(f"{ind}    for (anvil_h{c.id} = (int)({start}); anvil_h{c.id} < stop_; {step_twin}anvil_h{c.id} += {st.step}) {{")
             out.append(f"{ind}        anvil_mark({name});")
-            out += self.block(st.body, ind + "        ")
+            out += self.block(st.body, ind + "        ", in_loop=True, tail=tail)
             out.append(f"{ind}    }}")
         else:
             d = self.dev(c)
@@ -388,7 +491,7 @@ class HipGen:
             out.append(f"{ind}        anvil_write_i32({d}, (int)c_);")
             out.append(f"@@dirty {c.id} {ind}        ")
             out.append(f"{ind}        anvil_mark({name});")
-            out += self.block(st.body, ind + "        ")
+            out += self.block(st.body, ind + "        ", in_loop=True)
             out.append(f"{ind}    }}")
         out.append(f"{ind}}}")
         return out
@@ -512,6 +615,8 @@ class HipGen:
             r = b.root
             if r.init is not None and r.id in self.device_bufs:
                 self.mirror(r)
+        HSD_ID = 900_000_003
+        self.device_bufs[HSD_ID] = Buffer("host_scalars.device_copy", (max(1, len(self.hsd)),), I32, "scratch", id=HSD_ID)
         dev = sorted(self.device_bufs.values(), key=lambda b: b.id)
         plan = A.plan_arena(self.prog, dev, self.full_writer, share=os.environ.get("ANVIL_HIP_SHARE", "1") != "0",
                             fused=self.fused_group)
@@ -529,6 +634,10 @@ class HipGen:
             out.append(f"static {ctype(b.dtype)} anvil_h{bid};   // host scalar {b.name}")
         for b in sorted(self.mirrored.values(), key=lambda b: b.id):
             out.append(f"static anvil_mirror anvil_mir{b.id};")
+        out.append("static uint32_t *anvil_hsd;   // device copies of host scalars: " +
+                   ", ".join(f"[{i}] {self.by_id[bid].name}" for bid, i in sorted(self.hsd.items(), key=lambda t: t[1])))
+        for n in range(len(self.segments)):
+            out.append(f"static anvil_segment anvil_seg{n};")
         for b in self.prog.buffers:
             r = b.root
             if r is b and r.init is not None:
@@ -550,6 +659,7 @@ class HipGen:
         out.append(f"    anvil_device_open({plan.size});")
         for b in dev:
             out.append(f"    anvil_b{b.id} = ({ctype(b.dtype)} *)(anvil_dev.arena + {plan.offsets[b.id]});")
+        out.append(f"    anvil_hsd = (uint32_t *)anvil_b{HSD_ID};")
         for b in sorted(self.mirrored.values(), key=lambda b: b.id):
             out.append(f"    anvil_mirror_init(&anvil_mir{b.id}, (void **)&anvil_b{b.id}, {max(4, 4 * b.numel)});")
         for i, m in enumerate(self.faults, 1):
@@ -572,6 +682,20 @@ class HipGen:
         for bid in sorted(self.hosts):
             out.append(f"    anvil_h{bid} = 0;")
         out += ["    anvil_hs.seed = anvil_hs.seed0;", "    anvil_hs.stream = 0;", "    anvil_hs.t0 = anvil_seconds();", "}"]
+        def undirty(lines):
+            res = []
+            for line in lines:
+                if line.startswith("@@dirty "):
+                    _, bid, ind = line.split(" ", 2)
+                    if int(bid) in self.mirrored:
+                        res.append(f"{ind}anvil_mir{bid}.valid = 0;")
+                    continue
+                res.append(line)
+            return res
+        if self.segments:
+            out += ["", "// ---------------------------------------------------------------- graph segments"]
+            for fn in self.segments:
+                out += undirty(fn)
         out += ["", "// ---------------------------------------------------------------- the program",
                 "static int anvil_program(void) {"]
         for line in body:
@@ -651,6 +775,7 @@ class HipGen:
                 "int anvil_entry_device(void) {",
                 "    if (!anvil_dev.ready) { anvil_setup(); anvil_fresh(); }",
                 "    anvil_device_barrier();",
+                "    anvil_graphs.suspended = 1;",
                 "    anvil_hs.seed = anvil_hs.seed0; anvil_hs.stream = 0;"]
         for b in ins + outs:
             out.append(f"    {ctype(b.dtype)} *keep{b.id} = anvil_b{b.id};")
@@ -658,6 +783,7 @@ class HipGen:
             if b.id in self.mirrored:
                 out.append(f"    anvil_mir{b.id}.valid = 0;")
         out.append("    const int rc = anvil_program();")
+        out.append("    anvil_graphs.suspended = 0;")
         for b in ins + outs:
             out.append(f"    anvil_b{b.id} = keep{b.id};")
             if b.id in self.mirrored:
@@ -674,11 +800,16 @@ class HipGen:
 
 # ----------------------------------------------------------------------------- plugin API
 
-def generate(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False) -> str:
+def generate(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False,
+             graphs: bool | None = None) -> str:
     """The .hip source of a program (library=True: a function lowered by pyapi.lower, called
     through anvil_entry with the input/output slots). emulate=True: a CPU build of the same
-    program for testing the generator on a machine without a GPU."""
-    return HipGen(prog, seed=seed, library=library, emulate=emulate).generate()
+    program for testing the generator on a machine without a GPU. graphs=True: loop bodies are
+    captured into HIP graphs and replayed (default: $ANVIL_HIP_GRAPHS, else off — on MI355X with
+    ROCm 7.2 eager launches measured faster for the C2 training step)."""
+    if graphs is None:
+        graphs = os.environ.get("ANVIL_HIP_GRAPHS", "0") == "1"
+    return HipGen(prog, seed=seed, library=library, emulate=emulate, graphs=graphs).generate()
 
 
 def hipcc() -> str:
@@ -786,6 +917,6 @@ class HipLibrary:
 
 
 def load(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False,
-         rebuild: bool = False) -> HipLibrary:
-    src = generate(prog, seed=seed, library=library, emulate=emulate)
+         rebuild: bool = False, graphs: bool | None = None) -> HipLibrary:
+    src = generate(prog, seed=seed, library=library, emulate=emulate, graphs=graphs)
     return HipLibrary(compile_source(src, emulate=emulate, rebuild=rebuild), src)

@@ -351,7 +351,7 @@ class GemmPlan(Plan):
                     f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]
             value = "part[0][0][q]"
         stages = [(k, None, [])] + list(self.followers)
-        hoisted = self.hoistable(stages) if per * 4 <= 64 else []
+        hoisted = self.hoistable(stages) if per * 4 <= 64 and os.environ.get("ANVIL_GEMM_HOIST", "1") != "0" else []
         hoisted = hoisted[:max(0, 64 // per)]
 
         def element_vars(em):
@@ -398,7 +398,7 @@ class GemmPlan(Plan):
         body += ["    }", "}"]
         head = [self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
                 + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, B {self.bmode[9:]}",
-                self.header(self.threads) + " {"]
+                self.header(self.threads)]
         return "\n".join(head + body)
 
 

@@ -151,18 +151,41 @@ class Plan:
         self.hosts.setdefault(b.id, b)
         return f"h{b.id}"
 
+    def by_value(self) -> bool:
+        """Host scalars reach the kernel as arguments (eager launches), or from the device copy that
+        the host's scalar kernels' twins keep current (graph replay: arguments are frozen)."""
+        return not self.gen.graphs
+
     def params(self) -> str:
         ps = [f"uint32_t anvil_rs{i}" for i in range(max(1, len(self.streams)))] + ["uint32_t anvil_seed"]
-        ps += [f"{ctype(b.dtype)} h{b.id}" for b in self.hosts.values()]
+        if self.by_value():
+            ps += [f"{ctype(b.dtype)} h{b.id}" for b in self.hosts.values()]
+        elif self.hosts:
+            ps.append("uint32_t *__restrict__ anvil_hsd")
         ps += [f"{ctype(b.dtype)} *__restrict__ b{b.id}" for b in self.bufs.values()]
         return ", ".join(ps)
 
     def launch_args(self, stream_vars: list) -> list:
         sv = stream_vars or ["0u"]
         args = list(sv) + ["anvil_hs.seed"]
-        args += [f"anvil_h{b.id}" for b in self.hosts.values()]
+        if self.by_value():
+            args += [f"anvil_h{b.id}" for b in self.hosts.values()]
+        elif self.hosts:
+            args.append("anvil_hsd")
         args += [f"anvil_b{b.id}" for b in self.bufs.values()]
         return args
+
+    def host_prologue(self, mutable: bool = False) -> list[str]:
+        """Graph mode: host scalars, read from the device copy."""
+        out = []
+        if self.by_value():
+            return out
+        q = "" if mutable else "const "
+        for b in self.hosts.values():
+            slot = self.gen.hsd_slot(b)
+            v = f"(int)anvil_hsd[{slot}]" if b.dtype == I32 else f"anvil_f32_of(anvil_hsd[{slot}])"
+            out.append(f"    {q}{ctype(b.dtype)} h{b.id} = {v};")
+        return out
 
     def stream_param(self, k) -> str:
         return f"anvil_rs{self.streams.index(k)}" if k in self.streams else "anvil_rs0"
@@ -182,7 +205,9 @@ class Plan:
         return f"// {self.kind}: " + "; ".join(parts)
 
     def header(self, threads: int) -> str:
-        return f"__global__ void __launch_bounds__({threads}) {self.name}({self.params()})"
+        """The kernel's signature, its opening brace, and its host-scalar declarations."""
+        return "\n".join([f"__global__ void __launch_bounds__({threads}) {self.name}({self.params()}) {{"]
+                         + self.host_prologue())
 
     # body helpers
     def statements(self, em: Emitter, k: ir.Kernel, scope: KernelScope, parallel: bool, guard: str | None = None,
@@ -236,7 +261,7 @@ class MapPlan(Plan):
         for line in decode(k.domain, "u", it):
             em.emit(line)
         self.statements(em, k, sc, parallel=True)
-        head = [self.comment(), self.header(self.threads) + " {",
+        head = [self.comment(), self.header(self.threads),
                 f"    for ({it} u = ({it})blockIdx.x * {self.threads}u + threadIdx.x; u < {self.total}u; "
                 f"u += ({it})gridDim.x * {self.threads}u) {{"]
         return "\n".join(head + body + ["    }", "}"])
@@ -266,7 +291,7 @@ class SerialPlan(Plan):
         if k.red is not None:
             serial_reduction(em, sc, k, "        ")
         self.statements(em, k, sc, parallel=False)
-        head = [self.comment(), self.header(1) + " {",
+        head = [self.comment(), self.header(1),
                 f"    for (uint64_t u = 0; u < {self.total}ull; u++) {{"]
         return "\n".join(head + body + ["    }", "}"])
 
@@ -411,7 +436,7 @@ class RowsPlan(Plan):
             populated |= {key for key in self.cache_arrays}
         if L == THREADS:
             em.emit("__syncthreads();")
-        text = out + [self.header(self.threads) + " {"] + pre + shared
+        text = out + [self.header(self.threads)] + pre + shared
         text.append(f"    for (uint32_t row = {row0}; row < {self.R}u; row += {rstep}) {{")
         return "\n".join(text + body + ["    }", "}"])
 
@@ -595,7 +620,7 @@ class SplitPlan(Plan):
         em.emit("}")
         em.emit("__syncthreads();")
         head = [self.comment() + f" · {TX} outputs x {TY}-way split per workgroup",
-                self.header(THREADS) + " {",
+                self.header(THREADS),
                 f"    __shared__ {T} part[{TY}][{TX}];",
                 f"    const uint32_t tx = threadIdx.x % {TX}u, ty = threadIdx.x / {TX}u;",
                 f"    for (uint32_t rb = blockIdx.x * {TX}u; rb < {self.R}u; rb += gridDim.x * {TX}u) {{",
@@ -724,3 +749,44 @@ class GroupBuilder:
     def add(self, k):
         self.kernels.append(k)
         self._note(k)
+
+
+# ----------------------------------------------------------------------------- twins
+
+class TwinPlan(Plan):
+    """The device twin of a scalar kernel the host runs: it updates the device copy of the host
+    scalars (the array kernels read them from), so that a captured graph needs no host values."""
+
+    kind = "twin"
+
+    def by_value(self) -> bool:
+        return False
+
+    def __init__(self, gen, k, name):
+        super().__init__(gen, [k], name)
+        self.k = k
+
+    def source(self) -> str:
+        k = self.k
+        sc = KernelScope(self)
+        body: list[str] = []
+        em = Emitter(sc, body, "    ")
+        for st in k.stmts:
+            if isinstance(st, ir.Let):
+                em.let(st)
+                continue
+            val = em.store_value(st)
+            b = st.buf.root
+            h = sc.host_scalar(b)
+            slot = self.gen.hsd_slot(b)
+            bits = f"(uint32_t)({val})" if b.dtype == I32 else f"anvil_bits_of({val})"
+            em.emit(f"{h} = {val}; anvil_hsd[{slot}] = {bits};")
+            em.reset_memo()
+        for st in k.stores:                               # make sure it is a parameter
+            sc.host_scalar(st.buf.root)
+        head = [f"// twin of the host's {k.name}",
+                f"__global__ void __launch_bounds__(64) {self.name}({self.params()}) {{"] + self.host_prologue(True)
+        return "\n".join(head + ["    if (threadIdx.x != 0 || blockIdx.x != 0) return;"] + body + ["}"])
+
+    def grid(self):
+        return 1, 64

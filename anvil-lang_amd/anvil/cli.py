@@ -40,6 +40,8 @@ def main(argv=None) -> int:
         q.add_argument("program", help="a kernel-IR program (.json, anvil-ir/1)")
         q.add_argument("--seed", type=int, default=None, help="the random seed (default: the program's own)")
         q.add_argument("--emulate", action="store_true", help="a CPU build of the generated file (testing)")
+        q.add_argument("--graphs", action="store_true", default=None,
+                       help="replay loop bodies as HIP graphs (default: $ANVIL_HIP_GRAPHS)")
         if name in ("hip", "build"):
             q.add_argument("-o", "--output", default=None)
         if name == "run":
@@ -51,7 +53,7 @@ def main(argv=None) -> int:
     from .backend import hip
     prog, data = _load_program(args.program)
     seed = args.seed if args.seed is not None else int(data.get("seed", 0))
-    src = hip.generate(prog, seed=seed, emulate=args.emulate)
+    src = hip.generate(prog, seed=seed, emulate=args.emulate, graphs=args.graphs)
     if args.cmd == "hip":
         out = args.output or os.path.splitext(args.program)[0] + ".hip"
         with open(out, "w") as f:

@@ -21,6 +21,7 @@ the reference interpreter anvil/interp.py) timed on this host for a few full-siz
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -45,15 +46,33 @@ def load_program():
     return irjson.load(data), data
 
 
-def gpu_run(prog, data, steps: int, warmup: int):
+class quiet_stdout:
+    """The program prints (its loss); bench.py's stdout carries only the JSON line."""
+
+    def __enter__(self):
+        sys.stdout.flush()
+        self.saved = os.dup(1)
+        self.null = os.open(os.devnull, os.O_WRONLY)
+        os.dup2(self.null, 1)
+
+    def __exit__(self, *exc):
+        libc = ctypes.CDLL(None)
+        libc.fflush(None)
+        os.dup2(self.saved, 1)
+        os.close(self.null)
+        os.close(self.saved)
+
+
+def gpu_run(prog, data, steps: int, warmup: int, graphs: bool = False):
     from anvil.backend import hip
-    lib = hip.load(prog, seed=int(data.get("seed", 0)))
+    lib = hip.load(prog, seed=int(data.get("seed", 0)), graphs=graphs)
     # timed run
     lib.lib.anvil_marks_select(LOOP_COUNTER.encode())
     lib.lib.anvil_sync_device()
     t0 = time.perf_counter()
-    rc = lib.main()
-    lib.lib.anvil_sync_device()
+    with quiet_stdout():
+        rc = lib.main()
+        lib.lib.anvil_sync_device()
     wall = time.perf_counter() - t0
     if rc != 0:
         raise SystemExit(f"bench: the program exited with status {rc}")
@@ -65,8 +84,9 @@ def gpu_run(prog, data, steps: int, warmup: int):
     lib.lib.anvil_marks_select(b"")
     lib.lib.anvil_profile_enable(1)
     lib.lib.anvil_profile_reset()
-    lib.main()
-    lib.lib.anvil_sync_device()
+    with quiet_stdout():
+        lib.main()
+        lib.lib.anvil_sync_device()
     prof = lib.profile()
     lib.lib.anvil_profile_enable(0)
     return ms, wall, prof, lib
@@ -121,13 +141,14 @@ def main() -> int:
     p.add_argument("--cpu-steps", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--profile-table", action="store_true", help="print every kernel's time to stderr")
+    p.add_argument("--graphs", action="store_true", help="replay loop bodies as HIP graphs")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench: this build measures one GPU only (asked for {args.gpus}); the multi-GPU design is "
               "described in DESIGN.md and is not run", file=sys.stderr)
         return 2
     prog, data = load_program()
-    ms, wall, prof, lib = gpu_run(prog, data, args.steps, args.warmup)
+    ms, wall, prof, lib = gpu_run(prog, data, args.steps, args.warmup, graphs=args.graphs)
     if args.profile_table:
         for label, tms, calls, flops, nbytes in sorted(prof, key=lambda r: -r[1]):
             if calls:
@@ -143,6 +164,7 @@ def main() -> int:
         "config": {"workload": "C2: MLP 784-1024-1024-10, ReLU, cross_entropy, adam(lr=1e-3), batch 256, "
                                "shuffled, 500-step program", "global_batch": BATCH, "n_train": 65536,
                    "parallelism": "single GPU", "library": os.path.basename(lib.path),
+                   "graph_replay": args.graphs,
                    "program_wall_s": round(wall, 3)},
         "roofline": roofline(prof),
     }

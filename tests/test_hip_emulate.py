@@ -67,3 +67,17 @@ def test_checkpoint_save_then_load(tmp_path):
     assert out1.split("sum")[1] == out2.split("sum")[1]
     raw = (tmp_path / "w.ckpt").read_bytes()
     assert raw[:4] == b"EINW" and int.from_bytes(raw[4:8], "little") == 2 and len(raw) == 16 + 8 + 4 * 12
+
+
+@pytest.mark.parametrize("name", ["c2_small", "linreg", "control"])
+def test_graph_mode_matches_reference(name):
+    """Loop bodies captured as graph segments: host scalars reach kernels through their device copy,
+    kept current by the host scalar kernels' device twins (here run eagerly, on the CPU)."""
+    keep = kept_buffers(name)
+    rc, out, err, arrays = run_program(name, emulate=True, keep=keep, env_extra={"ANVIL_HIP_GRAPHS": "1"})
+    assert rc == 0, err
+    z = vectors(name)
+    problem = outputs_match(stdout_of(z), out, rtol=1e-3)
+    assert problem is None, problem
+    for k in keep:
+        assert tensors_match(z[f"buf:{k}"], arrays[k], rtol=1e-3) is None, k

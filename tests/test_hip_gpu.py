@@ -63,3 +63,17 @@ def test_gpu_checkpoint_save_then_load(tmp_path):
     assert rc1 == 0 and rc2 == 0, err1 + err2
     assert out1.startswith("loaded 0.0000") and out2.startswith("loaded 1.0000")
     assert out1.split("sum")[1] == out2.split("sum")[1]
+
+
+@pytest.mark.parametrize("name", ["c2_small", "linreg", "c4_small"])
+def test_gpu_graph_replay_matches_reference(name):
+    """The same programs with loop bodies captured once as HIP graphs and replayed."""
+    print(f"gpu graphs {name}", flush=True)
+    keep = kept_buffers(name)
+    rc, out, err, arrays = run_program(name, emulate=False, keep=keep, timeout=300, env_extra={"ANVIL_HIP_GRAPHS": "1"})
+    assert rc == 0, err
+    z = vectors(name)
+    problem = outputs_match(stdout_of(z), out, rtol=1e-3)
+    assert problem is None, problem
+    for k in keep:
+        assert tensors_match(z[f"buf:{k}"], arrays[k], rtol=1e-3) is None, k
