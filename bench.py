@@ -92,20 +92,76 @@ def gpu_run(prog, data, steps: int, warmup: int, graphs: bool = False):
     return ms, wall, prof, lib
 
 
-def roofline(prof):
+TRAFFIC = os.path.join(ROOT, "profiles", "c2_mlp_train_step_traffic.txt")
+
+
+def measured_traffic(library: str, kernel: str):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, calibrated with a copy kernel),
+    from the committed counter profile, if it was taken on this very library build; else None."""
+    try:
+        with open(TRAFFIC) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return None
+    if f"library {library}" not in lines:
+        return None
+    for line in lines:
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == kernel:
+            return int(parts[1]) + int(parts[2])
+    return None
+
+
+def roofline(prof, library: str):
     """The kernel with the most device time among those launched once per step."""
     rows = [r for r in prof if r[2] >= STEPS_IN_PROGRAM]
     label, ms, calls, flops, nbytes = max(rows, key=lambda r: r[1])
     t = ms / calls * 1e-3
+    traffic = measured_traffic(library, label.split()[0])
     if flops / max(nbytes, 1) > PEAK_FP32_MFMA / PEAK_HBM:
         achieved = flops / t / 1e12
         return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA / 1e12,
-                "unit": "TFLOP/s", "frac": round(achieved / (PEAK_FP32_MFMA / 1e12), 4), "traffic": None,
-                "kernel": label, "mean_us": round(t * 1e6, 3), "flops_per_launch": flops}
+                "unit": "TFLOP/s", "frac": round(achieved / (PEAK_FP32_MFMA / 1e12), 4), "traffic": traffic,
+                "kernel": label, "mean_us": round(t * 1e6, 3), "flops_per_launch": flops,
+                "algorithmic_bytes_per_launch": nbytes}
     achieved = nbytes / t / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(achieved / (PEAK_HBM / 1e9), 4), "traffic": None, "kernel": label,
+            "frac": round(achieved / (PEAK_HBM / 1e9), 4), "traffic": traffic, "kernel": label,
             "mean_us": round(t * 1e6, 3), "bytes_per_launch": nbytes}
+
+
+COPY_ELEMS = 1 << 24          # the calibration copy: 64 MiB read, 64 MiB written per launch
+COPY_LAUNCHES = 50
+
+
+def copy_program():
+    """An IR program whose loop is one plain copy kernel B[i] = A[i] of COPY_ELEMS floats: the
+    known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters into bytes."""
+    from anvil import ir
+    a = ir.Buffer("A", (COPY_ELEMS,), "f32", "param")
+    b = ir.Buffer("B", (COPY_ELEMS,), "f32", "param")
+    i, j = ir.Var("i", COPY_ELEMS), ir.Var("j", COPY_ELEMS)
+    fill = ir.Kernel([i], [ir.Store(a, ir.Affine(0, {i: 1}), ir.Rand(0))], name="fill", label="uniform")
+    copy = ir.Kernel([j], [ir.Store(b, ir.Affine(0, {j: 1}), ir.Load(a, ir.Affine(0, {j: 1})))], name="copy",
+                     label="copy")
+    it = ir.Buffer("it", (), "i32", "var")
+    main = ir.Block([ir.KernelStmt(fill), ir.For(it, 0, COPY_LAUNCHES, 1, ir.Block([ir.KernelStmt(copy)]))])
+    return ir.Program(main, [a, b, it])
+
+
+def copy_run() -> dict:
+    from anvil.backend import hip
+    lib = hip.load(copy_program())
+    lib.lib.anvil_marks_select(b"it")
+    with quiet_stdout():
+        lib.main()
+        lib.lib.anvil_sync_device()
+    n = lib.lib.anvil_marks_count()
+    ms = lib.lib.anvil_marks_elapsed_ms(5, n - 1) / (n - 6)
+    nbytes = 8 * COPY_ELEMS
+    return {"metric": "copy GB/s (calibration kernel)", "value": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
+            "bytes_per_launch": nbytes, "mean_us": round(ms * 1e3, 2), "launches": COPY_LAUNCHES,
+            "library": os.path.basename(lib.path)}
 
 
 def cpu_baseline(prog, data, steps: int):
@@ -142,7 +198,11 @@ def main() -> int:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--profile-table", action="store_true", help="print every kernel's time to stderr")
     p.add_argument("--graphs", action="store_true", help="replay loop bodies as HIP graphs")
+    p.add_argument("--copy", action="store_true", help="run the copy kernel that calibrates HBM counters")
     args = p.parse_args()
+    if args.copy:
+        print(json.dumps(copy_run()), flush=True)
+        return 0
     if args.gpus != 1:
         print(f"bench: this build measures one GPU only (asked for {args.gpus}); the multi-GPU design is "
               "described in DESIGN.md and is not run", file=sys.stderr)
@@ -166,7 +226,7 @@ def main() -> int:
                    "parallelism": "single GPU", "library": os.path.basename(lib.path),
                    "graph_replay": args.graphs,
                    "program_wall_s": round(wall, 3)},
-        "roofline": roofline(prof),
+        "roofline": roofline(prof, os.path.basename(lib.path)),
     }
     if not args.no_cpu:
         cpu = cpu_baseline(prog, data, args.cpu_steps)
