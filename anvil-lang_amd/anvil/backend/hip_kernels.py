@@ -48,6 +48,42 @@ def decode(vars_, src: str, it: str) -> list[str]:
     return out
 
 
+def unit_stride(k: ir.Kernel, v) -> bool:
+    """Does every memory access of k step by 0 or 1 element along v (so that 4 consecutive values
+    of v touch 4 consecutive floats: one wide load or store)?"""
+    for ld in A.kernel_loads(k):
+        if ld.offset.coef(v) not in (0, 1):
+            return False
+    for st in k.stores:
+        if st.offset.coef(v) not in (0, 1):
+            return False
+    return True
+
+
+def epilogue_loads(stages):
+    """(stage index, load) pairs of kernels' statements that may be issued before their reduction:
+    plain loads of buffers that no earlier statement stores to. stages: [(kernel, forwarded loads)]."""
+    stored: set = set()
+    out, seen = [], set()
+    for si, (e, fwd) in enumerate(stages):
+        fwd_ids = {id(ld) for ld in fwd}
+        canon = {v: ("e", v.id) for v in e.domain}
+        for st in e.stmts:
+            for ld in ir.loads_in(st.value):
+                b = ld.buf.root
+                if id(ld) in fwd_ids or not b.shape or b.id in stored or ld.offset.gathers():
+                    continue
+                if any(isinstance(t, ScalarRef) for t in ld.offset.terms):
+                    continue
+                key = (si, canon_key(ld.buf, ld.offset, canon))
+                if key not in seen:
+                    seen.add(key)
+                    out.append((si, ld))
+            if isinstance(st, ir.Store):
+                stored.add(st.buf.root.id)
+    return out
+
+
 def red_init(op: str, dtype: str) -> str:
     if op in ("sum",):
         return "0.0f" if dtype == F32 else "0"
@@ -249,7 +285,12 @@ class MapPlan(Plan):
         self.k = k
         self.total = ir.prod(v.extent for v in k.domain)
         self.threads = THREADS
-        self.blocks = max(1, min(-(-self.total // THREADS), MAX_BLOCKS))
+        # four consecutive elements per lane and step when every access is unit-stride along the
+        # innermost variable: the compiler merges them into 16-byte loads and stores
+        inner = k.domain[-1] if k.domain else None
+        self.V = 4 if (inner is not None and not gen.emulate and inner.extent % 4 == 0
+                       and unit_stride(k, inner)) else 1
+        self.blocks = max(1, min(-(-self.total // (THREADS * self.V)), MAX_BLOCKS))
 
     def source(self) -> str:
         k = self.k
@@ -257,14 +298,21 @@ class MapPlan(Plan):
         sc = KernelScope(self)
         sc.stream_name = self.stream_param(k)
         body: list[str] = []
-        em = Emitter(sc, body, "        ")
+        ind = "        " if self.V == 1 else "            "
+        em = Emitter(sc, body, ind)
         for line in decode(k.domain, "u", it):
             em.emit(line)
         self.statements(em, k, sc, parallel=True)
-        head = [self.comment(), self.header(self.threads),
-                f"    for ({it} u = ({it})blockIdx.x * {self.threads}u + threadIdx.x; u < {self.total}u; "
-                f"u += ({it})gridDim.x * {self.threads}u) {{"]
-        return "\n".join(head + body + ["    }", "}"])
+        n = self.total // self.V
+        head = [self.comment() + (f" · {self.V} elements per lane" if self.V > 1 else ""), self.header(self.threads),
+                f"    for ({it} w = ({it})blockIdx.x * {self.threads}u + threadIdx.x; w < {n}u; "
+                f"w += ({it})gridDim.x * {self.threads}u) {{"]
+        if self.V == 1:
+            head.append("        const auto u = w;")
+            return "\n".join(head + body + ["    }", "}"])
+        head += ["#pragma unroll", f"        for ({it} e = 0; e < {self.V}u; e++) {{",
+                 f"            const {it} u = {self.V}u * w + e;"]
+        return "\n".join(head + body + ["        }", "    }", "}"])
 
     def grid(self):
         return self.blocks, self.threads
@@ -344,7 +392,10 @@ class RowsPlan(Plan):
         self.R = ir.prod(v.extent for v in self.outer)
         self.n = ir.prod(self.inner_extents)
         self.L = lanes
-        self.Q = -(-self.n // lanes)
+        inner = head.red.vars[-1]
+        self.V = 4 if (lanes > 1 and not emulate and self.n % (4 * lanes) == 0 and inner.extent % 4 == 0
+                       and all(self._unit(k) for k in kernels)) else 1
+        self.Q = -(-self.n // (lanes * self.V))
         self.rpb = THREADS // lanes if lanes < THREADS else 1
         self.threads = THREADS if lanes > 1 else min(THREADS, max(64, 64 * -(-self.R // 64)))
         if lanes == 1:
@@ -354,6 +405,15 @@ class RowsPlan(Plan):
         self.cache_arrays: dict = {}       # canonical key -> array name
         self.emulate = emulate
         self.plan_cache()
+
+    def _unit(self, k) -> bool:
+        inner = k.red.vars[-1] if k.red is not None else (k.domain[-1] if len(k.domain) > len(self.outer) else None)
+        return inner is None or unit_stride(k, inner)
+
+    @property
+    def slot(self) -> str:
+        """The register-cache index of the current element."""
+        return "q" if self.V == 1 else f"(q * {self.V} + e)"
 
     # which element-level values live in registers between stages
     def stage_vars(self, k):
@@ -418,7 +478,7 @@ class RowsPlan(Plan):
         for line in decode(self.outer, "row", "uint32_t"):
             em.emit(line)
         for key, name in self.cache_arrays.items():
-            em.emit(f"{ctype(self._key_dtype(key))} {name}[{Q}];")
+            em.emit(f"{ctype(self._key_dtype(key))} {name}[{Q * self.V}];")
         populated: set = set()
         fwd: dict = {}
         for si, k in enumerate(self.kernels):
@@ -429,11 +489,12 @@ class RowsPlan(Plan):
                 sc.names[v] = f"v{self.outer[i].id}"
             sc.canon = cm
             sc.stream_name = self.stream_param(k)
+            self.populated_now = set()
             if k.red is not None:
                 self.reduction_stage(em, sc, k, si, shared, fwd, populated)
             else:
                 self.map_stage(em, sc, k, si, fwd, populated)
-            populated |= {key for key in self.cache_arrays}
+            populated |= self.populated_now
         if L == THREADS:
             em.emit("__syncthreads();")
         text = out + [self.header(self.threads)] + pre + shared
@@ -453,25 +514,43 @@ class RowsPlan(Plan):
 
     def element_loop(self, em: Emitter, inner_vars, body_fn):
         """for q: j = lane + L*q; decode the inner vars; body_fn(q)."""
-        L, Q, n = self.L, self.Q, self.n
+        L, Q, n, V = self.L, self.Q, self.n, self.V
         saved_memo = em.memo
         if self.cached:
             em.emit("#pragma unroll")
             em.emit(f"for (int q = 0; q < {Q}; q++) {{")
             em.ind += "    "
-            em.emit(f"const uint32_t j = (uint32_t)lane + {L}u * (uint32_t)q;")
-            if n % L:
+            if V > 1:
+                em.emit("#pragma unroll")
+                em.emit(f"for (int e = 0; e < {V}; e++) {{")
+                em.ind += "    "
+                em.emit(f"const uint32_t j = {V}u * ((uint32_t)lane + {L}u * (uint32_t)q) + (uint32_t)e;")
+            else:
+                em.emit(f"const uint32_t j = (uint32_t)lane + {L}u * (uint32_t)q;")
+            if n % (L * V):
                 em.emit(f"if (j < {n}u) {{")
                 em.ind += "    "
         else:
-            em.emit(f"for (uint32_t j = (uint32_t)lane; j < {n}u; j += {L}u) {{")
-            em.ind += "    "
+            if V > 1:
+                em.emit(f"for (uint32_t jv = (uint32_t)lane; jv < {n // V}u; jv += {L}u) {{")
+                em.ind += "    "
+                em.emit("#pragma unroll")
+                em.emit(f"for (uint32_t e = 0; e < {V}u; e++) {{")
+                em.ind += "    "
+                em.emit(f"const uint32_t j = {V}u * jv + e;")
+            else:
+                em.emit("#pragma unroll 8")
+                em.emit(f"for (uint32_t j = (uint32_t)lane; j < {n}u; j += {L}u) {{")
+                em.ind += "    "
         em.memo = dict(saved_memo)
         for line in decode(inner_vars, "j", "uint32_t"):
             em.emit(line)
         body_fn()
         em.memo = saved_memo
-        if self.cached and n % L:
+        if self.cached and n % (L * V):
+            em.ind = em.ind[:-4]
+            em.emit("}")
+        if V > 1:
             em.ind = em.ind[:-4]
             em.emit("}")
         em.ind = em.ind[:-4]
@@ -482,12 +561,14 @@ class RowsPlan(Plan):
         table = dict(fwd)
         for key, name in self.cache_arrays.items():
             if key in populated or key in fwd:
-                table[key] = fwd.get(key, f"{name}[q]")
+                table[key] = fwd.get(key, f"{name}[{self.slot}]")
             else:
                 def first_load(ld, name=name, key=key):
                     v = em.build(ld)
-                    em.emit(f"{name}[q] = {v};")
-                    return f"{name}[q]"
+                    em.emit(f"{name}[{self.slot}] = {v};")
+                    sc.fwd[key] = f"{name}[{self.slot}]"
+                    self.populated_now.add(key)
+                    return f"{name}[{self.slot}]"
                 table[key] = first_load
         sc.fwd = table
 
@@ -554,9 +635,10 @@ class RowsPlan(Plan):
                     return
                 name = self.cache_arrays.get(key)
                 if name is not None:
-                    em.emit(f"{name}[q] = {val};")
-                    fwd[key] = f"{name}[q]"
-                    sc.fwd[key] = f"{name}[q]"
+                    em.emit(f"{name}[{self.slot}] = {val};")
+                    fwd[key] = f"{name}[{self.slot}]"
+                    sc.fwd[key] = f"{name}[{self.slot}]"
+                    self.populated_now.add(key)
             self.statements(em, k, sc, parallel=True, on_store=on_store)
         self.element_loop(em, inner, body)
 
@@ -593,9 +675,20 @@ class SplitPlan(Plan):
         em = Emitter(sc, body, "        ")
         for line in decode(k.domain, "row", "uint32_t"):
             em.emit(line)
+        # the statements' own operands (an optimizer's state) are loaded before the reduction
+        pre = epilogue_loads([(k, [])])[:8]
+        canon = {v: ("e", v.id) for v in k.domain}
+        if pre:
+            em.emit(" ".join(f"float pre{i} = 0.0f;" if ld.buf.dtype == F32 else f"int pre{i} = 0;"
+                             for i, (_, ld) in enumerate(pre)))
+            em.emit(f"if (ty == 0 && row < {self.R}u) {{")
+            for i, (_, ld) in enumerate(pre):
+                em.emit(f"    pre{i} = {em.build(ld)};")
+            em.emit("}")
         em.emit(f"{T} acc = {red_init(op, dt)};")
         em.emit(f"if (row < {self.R}u) {{")
         em.ind += "    "
+        em.emit("#pragma unroll 8")
         em.emit(f"for (uint32_t j = ty; j < {self.n}u; j += {TY}u) {{")
         em.ind += "    "
         saved = em.memo
@@ -615,7 +708,12 @@ class SplitPlan(Plan):
         em.ind += "    "
         em.emit("acc = part[0][tx];")
         em.emit(f"for (int p = 1; p < {TY}; p++) acc = {red_combine(op, dt, 'acc', 'part[p][tx]')};")
+        if pre:
+            sc.canon = canon
+            sc.fwd = {canon_key(ld.buf, ld.offset, canon): f"pre{i}" for i, (_, ld) in enumerate(pre)}
+        em.reset_memo()
         self.statements(em, k, sc, parallel=True)
+        sc.canon, sc.fwd = None, {}
         em.ind = em.ind[:-4]
         em.emit("}")
         em.emit("__syncthreads();")

@@ -138,13 +138,13 @@ def copy_program():
     """An IR program whose loop is one plain copy kernel B[i] = A[i] of COPY_ELEMS floats: the
     known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters into bytes."""
     from anvil import ir
-    a = ir.Buffer("A", (COPY_ELEMS,), "f32", "param")
-    b = ir.Buffer("B", (COPY_ELEMS,), "f32", "param")
-    i, j = ir.Var("i", COPY_ELEMS), ir.Var("j", COPY_ELEMS)
-    fill = ir.Kernel([i], [ir.Store(a, ir.Affine(0, {i: 1}), ir.Rand(0))], name="fill", label="uniform")
+    a = ir.Buffer("A", (COPY_ELEMS,), "f32", "param", id=1)           # fixed ids: the same source,
+    b = ir.Buffer("B", (COPY_ELEMS,), "f32", "param", id=2)           # so the same built library,
+    i, j = ir.Var("i", COPY_ELEMS, id=3), ir.Var("j", COPY_ELEMS, id=4)  # in every process
+    fill = ir.Kernel([i], [ir.Store(a, ir.Affine(0, {i: 1}), ir.Rand(0))], name="fill", label="uniform", id=5)
     copy = ir.Kernel([j], [ir.Store(b, ir.Affine(0, {j: 1}), ir.Load(a, ir.Affine(0, {j: 1})))], name="copy",
-                     label="copy")
-    it = ir.Buffer("it", (), "i32", "var")
+                     label="copy", id=6)
+    it = ir.Buffer("it", (), "i32", "var", id=7)
     main = ir.Block([ir.KernelStmt(fill), ir.For(it, 0, COPY_LAUNCHES, 1, ir.Block([ir.KernelStmt(copy)]))])
     return ir.Program(main, [a, b, it])
 
@@ -162,6 +162,66 @@ def copy_run() -> dict:
     return {"metric": "copy GB/s (calibration kernel)", "value": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
             "bytes_per_launch": nbytes, "mean_us": round(ms * 1e3, 2), "launches": COPY_LAUNCHES,
             "library": os.path.basename(lib.path)}
+
+
+C3 = ["c3_softmax", "c3_layernorm", "c3_linear", "c3_attention"]
+
+
+class DeviceArray:
+    """A device allocation through the HIP runtime itself (no framework needed): inputs are
+    resident in HBM before the timed calls, as the metric asks."""
+
+    hip = None
+
+    def __init__(self, host):
+        if DeviceArray.hip is None:
+            DeviceArray.hip = ctypes.CDLL("libamdhip64.so")
+        self.nbytes = host.nbytes
+        self.ptr = ctypes.c_void_p()
+        if DeviceArray.hip.hipMalloc(ctypes.byref(self.ptr), ctypes.c_size_t(max(self.nbytes, 4))) != 0:
+            raise SystemExit("bench: hipMalloc failed")
+        DeviceArray.hip.hipMemcpy(self.ptr, host.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(self.nbytes), 1)
+
+    def data_ptr(self):
+        return self.ptr.value
+
+
+def c3_run(calls: int) -> dict:
+    """Config C3: each anvil.function at its BASELINE size, inputs ~N(0,1) (seed 2) already on the
+    device; every generated kernel timed with dispatch events over `calls` calls."""
+    import numpy as np
+    from anvil import irjson
+    from anvil.hip_function import Compiled, Lowered
+    out = {}
+    for name in C3:
+        with open(os.path.join(ROOT, "tests", "golden", "ir", f"{name}.json")) as f:
+            data = json.load(f)
+        prog = irjson.load(data)
+        low = Lowered.from_fixture(prog, data)
+        fn = Compiled(name, low, seed=int(data.get("seed", 0)))
+        rng = np.random.default_rng(2)
+        args = [DeviceArray(rng.standard_normal(b.shape).astype(np.float32)) for b in low.inputs]
+        res = [DeviceArray(np.zeros(b.shape, np.float32)) for b in low.outputs]
+        fn.call_device([a.data_ptr() for a in args], [r.data_ptr() for r in res])      # warm-up
+        fn.lib.lib.anvil_profile_enable(1)
+        fn.lib.lib.anvil_profile_reset()
+        for _ in range(calls):
+            fn.call_device([a.data_ptr() for a in args], [r.data_ptr() for r in res])
+        kernels = []
+        for label, ms, n, flops, nbytes in fn.lib.profile():
+            if n == 0:
+                continue
+            t = ms / n * 1e-3
+            mfma = flops / max(nbytes, 1) > PEAK_FP32_MFMA / PEAK_HBM
+            ach = flops / t / 1e12 if mfma else nbytes / t / 1e9
+            peak = PEAK_FP32_MFMA / 1e12 if mfma else PEAK_HBM / 1e9
+            kernels.append({"kernel": label, "mean_us": round(t * 1e6, 2), "bound": "mfma" if mfma else "hbm",
+                            "achieved": round(ach, 2), "unit": "TFLOP/s" if mfma else "GB/s",
+                            "frac": round(ach / peak, 4), "flops": flops, "bytes": nbytes})
+        fn.lib.lib.anvil_profile_enable(0)
+        out[name] = {"us_per_call_kernels": round(sum(k["mean_us"] for k in kernels), 2), "kernels": kernels}
+    return {"metric": "C3 anvil.function kernels vs roofline (device-resident inputs)", "calls": calls,
+            "functions": out}
 
 
 def cpu_baseline(prog, data, steps: int):
@@ -199,9 +259,13 @@ def main() -> int:
     p.add_argument("--profile-table", action="store_true", help="print every kernel's time to stderr")
     p.add_argument("--graphs", action="store_true", help="replay loop bodies as HIP graphs")
     p.add_argument("--copy", action="store_true", help="run the copy kernel that calibrates HBM counters")
+    p.add_argument("--c3", action="store_true", help="config C3: the standalone functions, per kernel")
     args = p.parse_args()
     if args.copy:
         print(json.dumps(copy_run()), flush=True)
+        return 0
+    if args.c3:
+        print(json.dumps(c3_run(20)), flush=True)
         return 0
     if args.gpus != 1:
         print(f"bench: this build measures one GPU only (asked for {args.gpus}); the multi-GPU design is "
