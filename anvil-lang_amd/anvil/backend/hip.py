@@ -122,7 +122,8 @@ class HipGen:
         self.tables: list[str] = []
         self.plans: list = []
         self.plan_of: dict = {}           # first kernel id -> plan (a run of kernels shares one)
-        self.group_of: dict = {}          # kernel id -> the plan it is a stage of
+        self.group_of: dict = {}          # kernel id -> the launch (plan) it is part of
+        self.part_of: dict = {}           # kernel id -> the kernel (plan) of that launch it is a stage of
         self.device_bufs: dict[int, Buffer] = {}
         self.mirrored: dict[int, Buffer] = {}
         self.ckpts: list[str] = []
@@ -253,6 +254,70 @@ class HipGen:
         self.mark_dead_stores(plan)
         return plan, j - i
 
+    def side_by_side(self, stmts, i, plan, used):
+        """Join the launches after `plan` that are independent of it (and of each other) into one
+        FusedPlan. Host scalar kernels between them then run before the launch: only if no part
+        before them reads what they write. Parts must agree on the workgroup size (a split kernel
+        is re-planned to it) unless they have no barrier; their LDS adds up."""
+        if self.emulate or os.environ.get("ANVIL_HIP_SIDE", "1") == "0":
+            return plan, used
+        ids = lambda bs: {b.root.id for b in bs}
+
+        def rw(p):
+            r, w = set(), set()
+            for k in p.kernels:
+                r |= ids(A.kernel_reads(k))
+                w |= ids(A.kernel_writes(k))
+            return r, w
+        parts = [plan]
+        hoisted = list(getattr(plan, "hoisted", []))
+        reads, writes = rw(plan)
+        threads = plan.grid()[1]
+        lds = HK.lds_bytes(plan)
+        j = i + used
+        taken = used
+        between: list = []
+        while j < len(stmts) and isinstance(stmts[j], KernelStmt) and len(parts) < 8:
+            k = stmts[j].kernel
+            if A.is_host_kernel(k, self.hosts):
+                between.append(k)
+                j += 1
+                continue
+            cand, cused = self.plan_run(stmts, j)
+            if cand.kind in ("serial", "fused"):
+                break
+            moved = between + list(getattr(cand, "hoisted", []))
+            if {st.buf.root.id for h in moved for st in h.stores} & reads:
+                break
+            cr, cw = rw(cand)
+            if cw & (reads | writes) or cr & writes:
+                break
+            t = max(threads, cand.grid()[1])
+            fixed = []
+            for p in parts + [cand]:
+                if p.grid()[1] == t or HK.barrier_free(p):
+                    fixed.append(p)
+                elif p.kind == "split" and t % p.TY == 0:
+                    q = HK.SplitPlan(self, p.k, p.name, p.TY, threads=t)
+                    q.skip_stores = p.skip_stores
+                    fixed.append(q)
+                else:
+                    break
+            if len(fixed) < len(parts) + 1:
+                break
+            if sum(HK.lds_bytes(p) for p in fixed) > 96 * 1024:
+                break
+            parts, threads = fixed, t
+            hoisted += moved
+            between = []
+            reads |= cr
+            writes |= cw
+            j += cused
+            taken = j - i
+        if len(parts) == 1:
+            return plan, used
+        return HK.FusedPlan(self, parts, "f" + plan.name, hoisted), taken
+
     def absorb_followers(self, plan, stmts, j) -> int:
         """Elementwise kernels right after a product (past host-only scalar kernels, which are then
         computed before the launch) that can run in its epilogue; returns the statements taken."""
@@ -360,10 +425,13 @@ class HipGen:
                 plan = self.plan_of.get(k.id)
                 if plan is None:
                     plan, used = self.plan_run(stmts, i)
+                    plan, used = self.side_by_side(stmts, i, plan, used)
                     self.plans.append(plan)
                     self.plan_of[k.id] = (plan, used)
-                    for kk in plan.kernels:
-                        self.group_of[kk.id] = plan
+                    for part in getattr(plan, "parts", [plan]):
+                        for kk in part.kernels:
+                            self.group_of[kk.id] = plan
+                            self.part_of[kk.id] = part
                 else:
                     plan, used = plan
                 for hk in getattr(plan, "hoisted", []):
@@ -710,15 +778,16 @@ class HipGen:
         return "\n".join(out) + "\n"
 
     def fused_group(self, k):
-        got = self.group_of.get(k.id)
-        if got is None:
+        """(launch key, buffers k's own kernel writes) when k is one of several IR kernels of a launch."""
+        plan = self.group_of.get(k.id)
+        if plan is None or len(plan.kernels) < 2:
             return None
-        plan = got
-        if len(plan.kernels) < 2:
-            return None
-        if not hasattr(plan, "_writes"):
-            plan._writes = plan.writes()
-        return id(plan), plan._writes
+        part = self.part_of[k.id]
+        if len(part.kernels) < 2:
+            return id(plan), set()          # alone in its part: its reads are its own inputs
+        if not hasattr(part, "_writes"):
+            part._writes = part.writes()
+        return id(plan), part._writes
 
     def full_writer(self, st, b) -> bool:
         if isinstance(st, KernelStmt):

@@ -322,9 +322,11 @@ def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = T
     pos = 0
     by_id = {b.id: b for b in device_bufs}
 
+    here = [0]                                          # the position uses are noted at
+
     def note(b, chain, write=False, full=False):
         if b.id in by_id:
-            uses.setdefault(b.id, []).append((pos, chain, write, full))
+            uses.setdefault(b.id, []).append((here[0], chain, write, full))
 
     def block(blk, chain):
         for st in blk.stmts:
@@ -333,6 +335,7 @@ def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = T
     def stmt(st, chain):
         nonlocal pos
         pos += 1
+        here[0] = pos
         if isinstance(st, ir.For):
             start = pos
             for b in (st.start, st.stop):
@@ -347,6 +350,7 @@ def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = T
             inner = chain + (("loop", id(st)),)
             block(st.cond_block, inner)
             pos += 1
+            here[0] = pos
             note(st.cond.root, inner)
             block(st.body, inner)
             pos += 1
@@ -363,17 +367,13 @@ def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = T
             own: set = set()
             if group is not None:
                 key, own = group
-                if last_group[0] == key:
-                    pos -= 1                            # a later stage of the kernel just noted
-                last_group[0] = key
-            else:
-                last_group[0] = None
+                here[0] = group_pos.setdefault(key, pos)    # every part of one launch: one position
             for b in stmt_reads(st):
                 if b not in own:
                     note(b, chain)
             for b in stmt_writes(st):
                 note(b, chain, write=True, full=full_writer(st, b))
-    last_group = [None]
+    group_pos: dict = {}
     block(prog.main, ())
 
     def lifetime(us):

@@ -280,6 +280,12 @@ class GemmPlan(Plan):
                     stored.add(st.buf.root.id)
         return out
 
+    def template_lds(self) -> int:
+        """LDS of the anvil_mfma.h templates the kernel instantiates."""
+        if self.sched == "tile":
+            return 2 * 4 * 16 * ((self.BM + 4) + (self.BN + 4))
+        return self.waves * 16 * 64 * 4
+
     def absorb(self, e, how):
         m, fwd = how
         self.followers.append((e, m, fwd))

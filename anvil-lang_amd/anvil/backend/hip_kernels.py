@@ -13,10 +13,13 @@
           lanes of a wavefront take neighbouring outputs (coalesced loads) and a workgroup splits
           each output's reduction TY ways, combining the partial results through LDS in a fixed
           order.
+  fused   independent kernels (no data between them) launched as one grid, side by side.
 
 Each plan produces the kernel's source and the host-side launch: grid, block and arguments.
 """
 from __future__ import annotations
+
+import re
 
 from .. import ir
 from ..ir import F32, I32, Gather, Load, ScalarRef, Var
@@ -653,13 +656,14 @@ class SplitPlan(Plan):
 
     kind = "split"
 
-    def __init__(self, gen, k, name, ty: int):
+    def __init__(self, gen, k, name, ty: int, threads: int = THREADS):
         super().__init__(gen, [k], name)
         self.k = k
         self.R = ir.prod(v.extent for v in k.domain)
         self.n = ir.prod(v.extent for v in k.red.vars)
         self.TY = ty
-        self.TX = THREADS // ty
+        self.threads = threads
+        self.TX = threads // ty
         self.blocks = max(1, min(-(-self.R // self.TX), MAX_BLOCKS))
 
     def source(self) -> str:
@@ -718,7 +722,7 @@ class SplitPlan(Plan):
         em.emit("}")
         em.emit("__syncthreads();")
         head = [self.comment() + f" · {TX} outputs x {TY}-way split per workgroup",
-                self.header(THREADS),
+                self.header(self.threads),
                 f"    __shared__ {T} part[{TY}][{TX}];",
                 f"    const uint32_t tx = threadIdx.x % {TX}u, ty = threadIdx.x / {TX}u;",
                 f"    for (uint32_t rb = blockIdx.x * {TX}u; rb < {self.R}u; rb += gridDim.x * {TX}u) {{",
@@ -726,7 +730,116 @@ class SplitPlan(Plan):
         return "\n".join(head + body + ["    }", "}"])
 
     def grid(self):
-        return self.blocks, THREADS
+        return self.blocks, self.threads
+
+
+# ----------------------------------------------------------------------------- side by side
+
+def lds_bytes(plan) -> int:
+    """Static LDS of a plan's kernel: its own __shared__ arrays plus what its library templates use."""
+    src = plan._source if hasattr(plan, "_source") else plan.source()
+    plan._source = src
+    total = 0
+    for typ, dims in re.findall(r"__shared__\s+(\w+)\s+\w+((?:\[\d+\])+)", src):
+        total += 4 * ir.prod(int(d) for d in re.findall(r"\d+", dims))
+    return total + getattr(plan, "template_lds", lambda: 0)()
+
+
+def barrier_free(plan) -> bool:
+    src = plan._source if hasattr(plan, "_source") else plan.source()
+    plan._source = src
+    return "__syncthreads" not in src and "__shared__" not in src
+
+
+def split_params(params: str) -> list[tuple[str, str]]:
+    out = []
+    for prm in params.split(", "):
+        typ, name = prm.rsplit(" ", 1)
+        out.append((typ, name))
+    return out
+
+
+class FusedPlan(Plan):
+    """Kernels with no data between them (none writes what another reads or writes) launched as one
+    grid: workgroup b runs workgroup b - start_j of part j, the part whose range of workgroups holds
+    b. Each part's kernel becomes a device function of its workgroup and grid coordinates. The
+    launch fills the chip with one part's tail and the next one's start instead of draining it
+    between launches, and a short part (a bias gradient) runs beside a long one (a weight gradient).
+    Parts use the fused workgroup's lanes; one with fewer lanes runs on the first ones, which it
+    may only do if it has no barrier."""
+
+    kind = "fused"
+
+    def __init__(self, gen, parts, name, hoisted):
+        super().__init__(gen, [k for p in parts for k in p.kernels], name)
+        self.parts = parts
+        self.streams = [k for p in parts for k in p.streams]
+        self.label = " | ".join(f"{p.name} {p.kind}: {p.label}" for p in parts)
+        self.threads = max(p.grid()[1] for p in parts)
+        self.hoisted = hoisted
+        for p in parts:
+            self.skip_stores |= p.skip_stores
+
+    @staticmethod
+    def dims(p):
+        blocks, _ = p.grid()
+        return blocks if isinstance(blocks, tuple) else (blocks, 1, 1)
+
+    def part_params(self, j, p):
+        """(fused parameter name, type) of part j's parameters, in its order."""
+        out = []
+        for typ, name in split_params(p.params()):
+            out.append((f"{name}_{j}" if name.startswith("anvil_rs") else name, typ))
+        return out
+
+    def params(self) -> str:
+        seen: dict = {}
+        for j, p in enumerate(self.parts):
+            for name, typ in self.part_params(j, p):
+                seen.setdefault(name, typ)
+        return ", ".join(f"{typ} {name}" for name, typ in seen.items())
+
+    def launch_args(self, stream_vars: list) -> list:
+        seen: dict = {}
+        at = 0
+        for j, p in enumerate(self.parts):
+            sv = stream_vars[at:at + len(p.streams)]
+            at += len(p.streams)
+            for (name, _), arg in zip(self.part_params(j, p), p.launch_args(sv)):
+                seen.setdefault(name, arg)
+        return list(seen.values())
+
+    def grid(self):
+        return sum(ir.prod(self.dims(p)) for p in self.parts), self.threads
+
+    def source(self) -> str:
+        texts, calls = [], []
+        for j, p in enumerate(self.parts):
+            src = p._source if hasattr(p, "_source") else p.source()
+            _, t = p.grid()
+            head = f"__global__ void __launch_bounds__({t}) {p.name}("
+            assert head in src, p.name
+            src = src.replace(head, f"__device__ __forceinline__ void {p.name}_part(const uint3 anvil_b, "
+                                    f"const uint3 anvil_g, ", 1)
+            src = src.replace("blockIdx.", "anvil_b.").replace("gridDim.", "anvil_g.")
+            texts.append(src)
+            gx, gy, gz = self.dims(p)
+            n = gx * gy * gz
+            args = ", ".join(name for name, _ in self.part_params(j, p))
+            guard = "" if t == self.threads else f"if (threadIdx.x < {t}u) "
+            calls += [f"    if (b < {n}u) {{",
+                      f"        {guard}{p.name}_part(make_uint3(b % {gx}u, b / {gx}u % {gy}u, b / {gx * gy}u), "
+                      f"make_uint3({gx}u, {gy}u, {gz}u), {args});",
+                      "        return;",
+                      "    }",
+                      f"    b -= {n}u;"]
+        for p in self.parts:
+            self.bufs.update(p.bufs)
+            self.hosts.update(p.hosts)
+        head = [f"// fused: {', '.join(p.name for p in self.parts)} side by side",
+                f"__global__ void __launch_bounds__({self.threads}) {self.name}({self.params()}) {{",
+                "    uint32_t b = blockIdx.x;"]
+        return "\n\n".join(texts) + "\n" + "\n".join(head + calls[:-1] + ["}"])
 
 
 # ----------------------------------------------------------------------------- choosing
