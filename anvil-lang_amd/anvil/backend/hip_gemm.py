@@ -237,8 +237,15 @@ class GemmPlan(Plan):
             self.sched, self.BM, self.BN = "tile", 64, 64
         else:
             self.sched, self.BM, self.BN = "ksplit", 32, 32
-        # the K split: enough wavefronts that each one's share (a few 8-k chunks) is in flight at once
-        self.waves = 16 if s.K >= 512 else (8 if s.K >= 128 else 4)
+        # the K split. With K in 8-k chunks (anvil_mm_tile_kpipe), four wavefronts with two or four
+        # chunks in flight each measured best for batch-256 layers (fewer requests in flight than
+        # 8 or 16 wavefronts, and a shorter reduction through LDS); otherwise the older loop wants
+        # enough wavefronts that each one's share is in flight at once.
+        self.pipe = s.K % 8 == 0 and os.environ.get("ANVIL_GEMM_PIPE", "1") != "0"
+        if self.pipe:
+            self.waves = 4
+        else:
+            self.waves = 16 if s.K >= 512 else (8 if s.K >= 128 else 4)
         self.unroll = 4
         force = os.environ.get("ANVIL_GEMM_FORCE")       # tuning: "tile64" | "tile128" | "ksplit:W:U"
         if force:
@@ -249,6 +256,9 @@ class GemmPlan(Plan):
             else:
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.waves, self.unroll = int(parts[1]), int(parts[2])
+        self.pipe = self.pipe and self.sched == "ksplit"
+        nch = -(-(s.K // 8) // self.waves)                  # chunks per wave
+        self.depth = max(1, min(int(os.environ.get("ANVIL_GEMM_DEPTH", "2" if nch <= 32 else "4")), nch))
         self.threads = 64 * self.waves if self.sched == "ksplit" else 256
         self.tm = -(-s.M // self.BM)
         self.tn = -(-s.N // self.BN)
@@ -353,8 +363,17 @@ class GemmPlan(Plan):
                     "        const int ni = n0 + (lane & 31);",
                     f"        if (mi >= {s.M} || ni >= {s.N}) continue;"]
             slot = "q"
-            main = [f"    float part[1][1][{per}];",
-                    f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]
+            if self.pipe:
+                kargs = (f"pa, {s.a_rs}LL, {s.a_ks}LL, pb, {s.b_rs}LL, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, {s.K}, "
+                         "opa, opb")
+                chk = lambda n: "true" if n % 32 else "false"
+                nch = -(-(s.K // 8) // W)
+                main = [f"    float part[1][1][{per}];",
+                        f"    anvil_mm_tile_kpipe<{W}, 1, 1, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
+                        f"{chk(s.M)}, {chk(s.N)}>(part, {kargs});"]
+            else:
+                main = [f"    float part[1][1][{per}];",
+                        f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]
             value = "part[0][0][q]"
         stages = [(k, None, [])] + list(self.followers)
         hoisted = self.hoistable(stages) if per * 4 <= 64 and os.environ.get("ANVIL_GEMM_HOIST", "1") != "0" else []

@@ -262,4 +262,104 @@ __device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][16 / W
             }
 }
 
+// The same K split with a software pipeline (K a multiple of 8): the K range is cut into C 8-k
+// chunks, NCH consecutive ones per wave (the last busy wave may have fewer, later waves none). A
+// wave keeps D chunks of operands in flight: it waits only for the oldest, runs its 4 MFMAs, and
+// reuses those registers for the chunk D ahead, so the matrix cores start on the first data to
+// arrive instead of after the last. The chunk loop is unrolled (NCH is a compile-time constant):
+// straight-line code, where the compiler's wait counts are exact. Rows and columns past M / N are
+// zero (CHKM, CHKN: the tile may cross the edge); k is always in range.
+template <int MODE, bool CHK>
+__device__ __forceinline__ void anvil_chunk_load_k(float (&r)[4], const float *__restrict__ p, long long rs, long long ks,
+                                                   int t, int tmax, int k) {
+    if (CHK && t >= tmax) {
+        r[0] = r[1] = r[2] = r[3] = 0.f;
+        return;
+    }
+    if (MODE == ANVIL_LD_KC) {
+        const anvil_f32x4 v = *(const anvil_f32x4 *)(p + (long long)t * rs + k);
+        r[0] = v.x;
+        r[1] = v.y;
+        r[2] = v.z;
+        r[3] = v.w;
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; s++) r[s] = p[(long long)t * rs + (long long)(k + s) * ks];
+    }
+}
+
+template <int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, bool FULL, class OPA, class OPB>
+__device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
+                                                    const float *__restrict__ a, long long a_rs, long long a_ks,
+                                                    const float *__restrict__ b, long long b_rs, long long b_ks,
+                                                    int M, int N, int m0, int n0, int c0, int n, OPA opa, OPB opb) {
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    float ab[D][TM][4], bb[D][TN][4];
+#define ANVIL_KP_LOAD(d, c)                                                                                \
+    if (FULL || (c) < n) {                                                                                 \
+        const int k_ = 8 * (c0 + (c)) + 4 * h;                                                             \
+        _Pragma("unroll") for (int i = 0; i < TM; i++)                                                     \
+            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, a_rs, a_ks, m0 + 32 * i + r, M, k_);             \
+        _Pragma("unroll") for (int j = 0; j < TN; j++)                                                     \
+            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, b_rs, b_ks, n0 + 32 * j + r, N, k_);             \
+    }
+#pragma unroll
+    for (int c = 0; c < D; c++) ANVIL_KP_LOAD(c, c)
+    __builtin_amdgcn_sched_barrier(0);          // every load of the prologue is issued before the first MFMA
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        if (FULL || c < n) {
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(opa(ab[c % D][i][s]), opb(bb[c % D][j][s]),
+                                                                           acc.c[i][j], 0, 0, 0);
+        }
+        if (c + D < NCH) ANVIL_KP_LOAD(c % D, c + D)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#undef ANVIL_KP_LOAD
+}
+
+template <int W, int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, class OPA, class OPB>
+__device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W],
+                                                    const float *__restrict__ a, long long a_rs, long long a_ks,
+                                                    const float *__restrict__ b, long long b_rs, long long b_ks,
+                                                    int M, int N, int m0, int n0, int K, OPA opa, OPB opb) {
+    constexpr int PER = 16 / W;
+    __shared__ float part[W * TM * TN * 16 * 64];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     // uniform: scalar branches
+    const int c0 = w * NCH, n = min(NCH, max(0, (K >> 3) - c0));
+    anvil_mm_acc<TM, TN> acc;
+    acc.zero();
+    if (n == NCH)
+        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, true>(acc, a, a_rs, a_ks, b, b_rs, b_ks, M, N,
+                                                                            m0, n0, c0, n, opa, opb);
+    else if (n > 0)
+        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, false>(acc, a, a_rs, a_ks, b, b_rs, b_ks, M, N,
+                                                                             m0, n0, c0, n, opa, opb);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) part[(((w * TM + i) * TN + j) * 16 + v) * 64 + lane] = acc.c[i][j][v];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int q = 0; q < PER; q++) {
+                float s = 0.f;
+#pragma unroll
+                for (int src = 0; src < W; src++) s += part[(((src * TM + i) * TN + j) * 16 + PER * w + q) * 64 + lane];
+                out[i][j][q] = s;
+            }
+}
+
 #endif
