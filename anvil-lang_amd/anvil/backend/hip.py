@@ -106,6 +106,8 @@ class HostScope(Scope):
 class HipGen:
     def __init__(self, prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False,
                  graphs: bool = False):
+        if not emulate and os.environ.get("ANVIL_HIP_SINK", "1") != "0":
+            prog = A.sink_scalar_kernels(prog)
         self.prog = prog
         self.seed = seed & 0xFFFFFFFF
         self.library = library
@@ -227,6 +229,47 @@ class HipGen:
     # ------------------------------------------------------------------ planning kernels
     def plan_run(self, stmts: list, i: int):
         """The plan for the kernel at stmts[i] and how many statements it takes."""
+        got = self.row_block(stmts, i)
+        if got is not None:
+            return got
+        return self.plan_one(stmts, i)
+
+    def row_block(self, stmts: list, i: int):
+        """A RowBlockPlan for the chain of row-by-row kernels starting at stmts[i], if the chain
+        would otherwise take two launches or more."""
+        if self.emulate or os.environ.get("ANVIL_HIP_ROWBLOCK", "1") == "0":
+            return None
+        k = stmts[i].kernel
+        if not k.domain or not 64 <= k.domain[0].extent <= 4096:
+            return None
+        rb = HK.RowBlockBuilder(k.domain[0].extent)
+        j = i
+        while j < len(stmts) and isinstance(stmts[j], KernelStmt) and rb.fits(stmts[j].kernel, self.hosts):
+            j += 1
+        if j - i < 2:
+            return None
+        # only a chain: some stage reads what an earlier one wrote (independent kernels are
+        # better served side by side, each with its own schedule)
+        written: set = set()
+        chained = False
+        for kk in rb.kernels:
+            if {b.id for b in A.kernel_reads(kk)} & written:
+                chained = True
+            written |= {b.id for b in A.kernel_writes(kk)}
+        if not chained:
+            return None
+        launches, t = 0, i
+        while t < j:
+            p, used = self.plan_one(stmts, t)
+            if (p.kind == "gemm" and p.s.K >= 64) or p.kind == "split":
+                return None                     # a real product, or a strided reduction: keep its schedule
+            launches += 1
+            t += used
+        if launches < 2:
+            return None
+        return HK.RowBlockPlan(self, rb.kernels, f"k{k.id}", rb.R), j - i
+
+    def plan_one(self, stmts: list, i: int):
         k = stmts[i].kernel
         name = f"k{k.id}"
         parallel = A.parallel_safe(k)

@@ -255,6 +255,50 @@ def is_host_kernel(k: ir.Kernel, hosts: set) -> bool:
     return all(b.id in hosts or b.kind == "const" for b in kernel_reads(k))
 
 
+# ----------------------------------------------------------------------------- reordering
+
+def commutes(a: ir.Kernel, b: ir.Kernel) -> bool:
+    """May kernels a and b (a first) run in the other order? No buffer (or scalar) that one writes
+    is read or written by the other, and they do not both draw random numbers (each launch that
+    does takes the next stream number)."""
+    ra, wa = {x.id for x in kernel_reads(a)}, {x.id for x in kernel_writes(a)}
+    rb, wb = {x.id for x in kernel_reads(b)}, {x.id for x in kernel_writes(b)}
+    if wa & (rb | wb) or ra & wb:
+        return False
+    return not (a.uses_rand() and b.uses_rand())
+
+
+def sink_scalar_kernels(prog: ir.Program) -> ir.Program:
+    """The program with each kernel that produces one value (a loss, an accuracy: an empty domain)
+    moved later in its straight run of kernels, past every kernel it commutes with. A per-row
+    chain (logits, log-softmax, their gradient) then stays unbroken, and the moved kernel can share
+    a later launch. The caller's program is not changed (blocks are copied)."""
+    import dataclasses
+
+    def block(blk: ir.Block) -> ir.Block:
+        out = [stmt(st) for st in blk.stmts]
+        for idx in range(len(out) - 1, -1, -1):
+            st = out[idx]
+            if not (isinstance(st, KernelStmt) and not st.kernel.domain and st.kernel.red is not None):
+                continue
+            j = idx
+            while j + 1 < len(out) and isinstance(out[j + 1], KernelStmt) and commutes(st.kernel, out[j + 1].kernel):
+                j += 1
+            if j > idx:
+                out.insert(j, out.pop(idx))
+        return dataclasses.replace(blk, stmts=out)
+
+    def stmt(st):
+        if isinstance(st, ir.For):
+            return dataclasses.replace(st, body=block(st.body))
+        if isinstance(st, ir.While):
+            return dataclasses.replace(st, cond_block=block(st.cond_block), body=block(st.body))
+        if isinstance(st, ir.If):
+            return dataclasses.replace(st, then=block(st.then), orelse=block(st.orelse))
+        return st
+    return dataclasses.replace(prog, main=block(prog.main))
+
+
 # ----------------------------------------------------------------------------- program-wide reads
 
 def all_readers(prog: ir.Program) -> dict:

@@ -13,6 +13,8 @@
           lanes of a wavefront take neighbouring outputs (coalesced loads) and a workgroup splits
           each output's reduction TY ways, combining the partial results through LDS in a fixed
           order.
+  rowblock  a chain of kernels that work row by row (logits, log-softmax, its gradient, the next
+          layer's input gradient): one workgroup per row runs every stage of the chain.
   fused   independent kernels (no data between them) launched as one grid, side by side.
 
 Each plan produces the kernel's source and the host-side launch: grid, block and arguments.
@@ -350,8 +352,9 @@ class SerialPlan(Plan):
         return 1, 1
 
 
-def serial_reduction(em: Emitter, sc: KernelScope, k: ir.Kernel, ind: str) -> None:
-    """The reduction as nested loops in one lane (element order = the flattened row-major order)."""
+def serial_reduction(em: Emitter, sc: KernelScope, k: ir.Kernel, ind: str, unroll: bool = False) -> None:
+    """The reduction as nested loops in one lane (element order = the flattened row-major order).
+    unroll: unroll the loops (short ones fully), so that their loads are in flight together."""
     red = k.red
     op, dt = red.op, red.body.dtype
     T = ctype(dt)
@@ -362,6 +365,8 @@ def serial_reduction(em: Emitter, sc: KernelScope, k: ir.Kernel, ind: str) -> No
         em.emit(f"{T} acc = {red_init(op, dt)};")
     saved_ind = em.ind
     for v in red.vars:
+        if unroll:
+            em.emit("#pragma unroll" if v.extent <= 64 else "#pragma unroll 8")
         em.emit(f"for (int v{v.id} = 0; v{v.id} < {v.extent}; v{v.id}++) {{")
         em.ind += "    "
     saved = em.memo
@@ -731,6 +736,292 @@ class SplitPlan(Plan):
 
     def grid(self):
         return self.blocks, self.threads
+
+
+# ----------------------------------------------------------------------------- row blocks
+
+def row_local(off: ir.Affine, k: ir.Kernel, R: int, S: int | None) -> bool:
+    """Does `off` (an access of kernel k, whose first domain variable walks R rows of f0 values
+    each) stay inside row r's slice [r S, (r + 1) S) of its buffer, for every row r?"""
+    if S is None or off.scalars():
+        return False
+    v0 = k.domain[0]
+    f0 = v0.extent // R
+    if off.coef(v0) * f0 != S:
+        return False
+    lo = hi = off.const
+    for t, c in off.terms.items():
+        if isinstance(t, Var):
+            ext = f0 if t is v0 else (t.extent or 1)
+            span = c * (ext - 1)
+        elif isinstance(t, Gather):
+            g0, g1 = t.check_range()
+            lo += min(c * g0, c * (g1 - 1))
+            hi += max(c * g0, c * (g1 - 1))
+            continue
+        else:
+            return False
+        if span >= 0:
+            hi += span
+        else:
+            lo += span
+    return lo >= 0 and hi < S
+
+
+class RowBlockBuilder:
+    """A chain of consecutive kernels that all work row by row over the same R rows (the first
+    domain variable of each walks the rows), where every buffer the chain writes is only ever
+    touched in the row being processed: then one workgroup can run the whole chain for a row,
+    stage after stage, with a barrier in between and no launch between the stages."""
+
+    MAX_ROW_WORK = 1 << 15          # outputs x reduction length per row and stage
+
+    def __init__(self, R: int):
+        self.R = R
+        self.kernels: list = []
+        self.written: dict = {}     # buffer id -> row slice
+        self.far: set = set()       # buffers some stage reads outside its row
+        self.before: set = set()    # buffers read before the chain writes them (their old values)
+
+    def slice_of(self, b):
+        n = b.root.numel
+        return n // self.R if n % self.R == 0 else None
+
+    def fits(self, k: ir.Kernel, hosts: set) -> bool:
+        if not k.domain or A.is_host_kernel(k, hosts) or not A.parallel_safe(k):
+            return False
+        if k.domain[0].extent % self.R:
+            return False
+        E = ir.prod(v.extent for v in k.domain) // self.R
+        n = ir.prod(v.extent for v in k.red.vars) if k.red is not None else 1
+        if E * n > self.MAX_ROW_WORK:
+            return False
+        # a buffer whose old contents a stage reads is not written by the chain: the chain's
+        # launch is one position of the program for the arena, where the reads of buffers the
+        # launch writes are taken to be of the launch's own values
+        before = self.before | {b.id for b in A.kernel_reads(k) if b.id not in self.written}
+        written = dict(self.written)
+        for st in k.stores:
+            b = st.buf.root
+            S = self.slice_of(b)
+            if b.id in self.far or b.id in before or not row_local(st.offset, k, self.R, S):
+                return False
+            written[b.id] = S
+        far = set()
+        for ld in A.kernel_loads(k):
+            b = ld.buf.root
+            local = row_local(ld.offset, k, self.R, self.slice_of(b))
+            if b.id in written and not local:
+                return False
+            if not local:
+                far.add(b.id)
+        scal: set = set()
+        for e in k.exprs():
+            for x in ir.iter_expr(e):
+                if isinstance(x, Load):
+                    A.affine_scalars(x.offset, scal)
+        if any(b.id in written for b in scal):
+            return False
+        self.written = written
+        self.far |= far
+        self.before = before
+        self.kernels.append(k)
+        return True
+
+
+class RowBlockScope(KernelScope):
+    """Loads of the chain's own row slices kept in LDS read the LDS copy."""
+
+    def __init__(self, plan):
+        super().__init__(plan)
+        self.em = None
+
+    def override_load(self, ld):
+        b = ld.buf.root
+        if b.id in self.plan.shadow and self.em is not None:
+            S = self.plan.shadow[b.id]
+            return f"sh{b.id}[{self.em.affine(ld.offset, ld.buf)} - (int)row * {S}]"
+        return super().override_load(ld)
+
+
+class RowBlockPlan(Plan):
+    """One workgroup per row (of R) runs a chain of kernels stage by stage. A stage's outputs for
+    the row are spread over the workgroup: lane t takes outputs t, t + 256, ... and reduces each one
+    alone; a stage with a few outputs and a long reduction instead has every lane accumulate a
+    share of the reduction for all of the outputs (so an operand row is read once), the shares
+    then combined by shuffles and LDS in a fixed order. Each buffer the chain writes is written in
+    the row's own slice; a slice of up to SHADOW elements is also kept in LDS, where later stages
+    read it (and a buffer no kernel outside the chain reads is not written to memory at all). A
+    barrier separates the stages."""
+
+    kind = "rowblock"
+    SHADOW = 2048                   # elements of a row slice kept in LDS
+
+    def __init__(self, gen, kernels, name, R: int):
+        super().__init__(gen, kernels, name)
+        self.R = R
+        self.threads = THREADS
+        self.blocks = min(R, MAX_BLOCKS)
+        self.shadow: dict = {}      # buffer id -> row slice (kept in LDS)
+        self.dead: set = set()      # buffers only the chain reads: no memory copy
+        readers_in: dict = {}
+        for k in kernels:
+            for b in A.kernel_reads(k):
+                readers_in[b.id] = readers_in.get(b.id, 0) + 1
+        total = 0
+        for k in kernels:
+            for st in k.stores:
+                b = st.buf.root
+                if b.id in self.shadow:
+                    continue
+                S = b.numel // R
+                dead = (b.kind in A.SHARED_KINDS and not gen.is_host(b) and not getattr(b, "heap", False)
+                        and gen.readers.get(b.id, 0) == readers_in.get(b.id, 0))
+                accum = any(s2.accumulate and s2.buf.root is b for k2 in kernels for s2 in k2.stores)
+                if S > self.SHADOW or total + S > 8192 or (accum and not dead) or not readers_in.get(b.id):
+                    continue
+                self.shadow[b.id] = S
+                total += S
+                if dead:
+                    self.dead.add(b.id)
+
+    def grid(self):
+        return self.blocks, self.threads
+
+    def stage_statements(self, em, k, sc, guard=None):
+        for st in k.stmts:
+            if isinstance(st, ir.Let):
+                em.let(st)
+                continue
+            val = em.store_value(st)
+            b = st.buf.root
+            off = em.affine(st.offset, st.buf)
+            lines = []
+            if b.id in self.shadow:
+                sh = f"sh{b.id}[{off} - (int)row * {self.shadow[b.id]}]"
+                lines.append(f"atomicAdd(&{sh}, {val});" if st.accumulate else f"{sh} = {val};")
+            if b.id not in self.dead:
+                target = f"{sc.buf(st.buf)}[{off}]"
+                lines.append(f"atomicAdd(&{target}, {val});" if st.accumulate else f"{target} = {val};")
+            for line in lines:
+                em.emit(f"if ({guard}) {line}" if guard else line)
+            em.reset_memo()
+
+    def source(self) -> str:
+        T = self.threads
+        body: list[str] = []
+        shared: list[str] = []
+        for si, k in enumerate(self.kernels):
+            sc = RowBlockScope(self)
+            sc.stream_name = self.stream_param(k)
+            em = Emitter(sc, body, "        ")
+            sc.em = em
+            E = ir.prod(v.extent for v in k.domain) // self.R
+            sc.rand = f"(row * {E}u + e)"
+            red = k.red
+            n = ir.prod(v.extent for v in red.vars) if red is not None else 1
+            em.emit(f"// stage {si}: {k.name} ({E} per row" + (f", reduce {red.op} of {n}" if red else "") + ")")
+            if red is not None and red.op in RED_CODE and E <= 16 and n >= 256:
+                self.block_stage(em, sc, k, si, E, n, shared)
+                em.emit("__syncthreads();")
+                continue
+            wave = red is not None and red.op in RED_CODE and E < 64 and n > 64
+            trips = -(-E // (T // 64 if wave else T))          # outputs per wave / per lane
+            if trips > 1:
+                em.emit(f"#pragma unroll {min(4, trips)}")
+            if wave:
+                em.emit(f"for (uint32_t e = threadIdx.x >> 6; e < {E}u; e += {T // 64}u) {{")
+            else:
+                em.emit(f"for (uint32_t e = threadIdx.x; e < {E}u; e += {T}u) {{")
+            em.ind += "    "
+            for line in decode(k.domain, f"row * {E}u + e", "uint32_t"):
+                em.emit(line)
+            if red is None:
+                self.stage_statements(em, k, sc)
+            elif wave:
+                dt = red.body.dtype
+                ty = ctype(dt)
+                em.emit(f"{ty} acc = {red_init(red.op, dt)};")
+                em.emit("#pragma unroll 8")
+                em.emit(f"for (uint32_t j = lane; j < {n}u; j += 64u) {{")
+                em.ind += "    "
+                saved = em.memo
+                em.memo = dict(saved)
+                for line in decode(list(red.vars), "j", "uint32_t"):
+                    em.emit(line)
+                val = em.ex(red.body)
+                em.emit(f"acc = {red_combine(red.op, dt, 'acc', val)};")
+                em.memo = saved
+                em.ind = em.ind[:-4]
+                em.emit("}")
+                em.emit(f"acc = anvil_wave_all<{RED_CODE[red.op]}, {ty}>(acc);")
+                self.stage_statements(em, k, sc, guard="lane == 0")
+            else:
+                serial_reduction(em, sc, k, em.ind, unroll=True)
+                self.stage_statements(em, k, sc)
+            em.ind = em.ind[:-4]
+            em.emit("}")
+            em.emit("__syncthreads();")
+        for bid, S in self.shadow.items():
+            shared.append(f"    __shared__ {ctype(self.gen.by_id[bid].dtype)} sh{bid}[{S}];")
+        head = [self.comment() + f" · one workgroup per row, {self.R} rows", self.header(T)] + shared + [
+                "    const uint32_t lane = threadIdx.x & 63u;",
+                "    (void)lane;",
+                f"    for (uint32_t row = blockIdx.x; row < {self.R}u; row += gridDim.x) {{"]
+        return "\n".join(head + body + ["    }", "}"])
+
+    def block_stage(self, em, sc, k, si, E, n, shared):
+        """Every lane accumulates its share of the reduction for each of the E outputs; wave
+        shuffles, then LDS across the four waves (in wave order), give the sums; lane e finishes
+        output e."""
+        T = self.threads
+        red = k.red
+        dt = red.body.dtype
+        ty = ctype(dt)
+        shared.append(f"    __shared__ {ty} part{si}[{T // 64}][{E}];")
+        em.emit("{")
+        em.ind += "    "
+        em.emit(f"{ty} acc[{E}];")
+        em.emit(f"for (int q = 0; q < {E}; q++) acc[q] = {red_init(red.op, dt)};")
+        em.emit("#pragma unroll 4")
+        em.emit(f"for (uint32_t j = threadIdx.x; j < {n}u; j += {T}u) {{")
+        em.ind += "    "
+        for line in decode(list(red.vars), "j", "uint32_t"):
+            em.emit(line)
+        for q in range(E):
+            em.emit("{")
+            em.ind += "    "
+            saved = em.memo
+            em.memo = {}
+            em.emit(f"const uint32_t e = {q}u;")
+            for line in decode(k.domain, f"row * {E}u + e", "uint32_t"):
+                em.emit(line)
+            val = em.ex(red.body)
+            em.emit(f"acc[{q}] = {red_combine(red.op, dt, f'acc[{q}]', val)};")
+            em.memo = saved
+            em.ind = em.ind[:-4]
+            em.emit("}")
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        em.emit(f"for (int q = 0; q < {E}; q++) {{")
+        em.emit(f"    const {ty} w_ = anvil_wave_all<{RED_CODE[red.op]}, {ty}>(acc[q]);")
+        em.emit(f"    if (lane == 0) part{si}[threadIdx.x >> 6][q] = w_;")
+        em.emit("}")
+        em.emit("__syncthreads();")
+        em.emit(f"if (threadIdx.x < {E}u) {{")
+        em.ind += "    "
+        em.emit("const uint32_t e = threadIdx.x;")
+        for line in decode(k.domain, f"row * {E}u + e", "uint32_t"):
+            em.emit(line)
+        em.emit(f"{ty} acc_s = part{si}[0][e];")
+        em.emit(f"for (int w = 1; w < {T // 64}; w++) acc_s = {red_combine(red.op, dt, 'acc_s', f'part{si}[w][e]')};")
+        sc.acc_name = "acc_s"
+        em.reset_memo()
+        self.stage_statements(em, k, sc)
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        em.ind = em.ind[:-4]
+        em.emit("}")
 
 
 # ----------------------------------------------------------------------------- side by side
