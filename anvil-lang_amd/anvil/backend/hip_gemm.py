@@ -247,24 +247,34 @@ class GemmPlan(Plan):
         else:
             self.waves = 16 if s.K >= 512 else (8 if s.K >= 128 else 4)
         self.unroll = 4
-        force = os.environ.get("ANVIL_GEMM_FORCE")       # tuning: "tile64" | "tile128" | "ksplit:W:U"
-        if force:
+        ca, cb = s.la.offset.coef, s.lb.offset.coef
+        self.amode = load_mode(s.a_rs, s.a_ks, s.M, s.K, s.la.offset.const, [ca(v) for v in s.batch])
+        self.bmode = load_mode(s.b_rs, s.b_ks, s.N, s.K, s.lb.offset.const, [cb(v) for v in s.batch])
+        self.slab = 0
+        # tuning: $ANVIL_GEMM_FORCE = comma-separated "tile64" | "tile128" | "ksplit:W:U" | "slab:KC",
+        # each optionally "@NN" / "@NT" / "@TN" (only products whose operands load that way)
+        layout = {("ANVIL_LD_KC", "ANVIL_LD_RC"): "NN", ("ANVIL_LD_KC", "ANVIL_LD_KC"): "NT",
+                  ("ANVIL_LD_RC", "ANVIL_LD_RC"): "TN"}.get((self.amode, self.bmode), "?")
+        for force in os.environ.get("ANVIL_GEMM_FORCE", "").split(","):
+            force, _, only = force.partition("@")
+            if not force or (only and only != layout):
+                continue
             parts = force.split(":")
             if parts[0].startswith("tile"):
                 self.sched, self.BM = "tile", int(parts[0][4:])
                 self.BN = self.BM
+            elif parts[0] == "slab":
+                self.sched, self.BM, self.BN = "ksplit", 32, 32
+                self.slab, self.waves = int(parts[1]), 4
             else:
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.waves, self.unroll = int(parts[1]), int(parts[2])
-        self.pipe = self.pipe and self.sched == "ksplit"
+        self.pipe = self.pipe and self.sched == "ksplit" and not self.slab
         nch = -(-(s.K // 8) // self.waves)                  # chunks per wave
         self.depth = max(1, min(int(os.environ.get("ANVIL_GEMM_DEPTH", "2" if nch <= 32 else "4")), nch))
         self.threads = 64 * self.waves if self.sched == "ksplit" else 256
         self.tm = -(-s.M // self.BM)
         self.tn = -(-s.N // self.BN)
-        ca, cb = s.la.offset.coef, s.lb.offset.coef
-        self.amode = load_mode(s.a_rs, s.a_ks, s.M, s.K, s.la.offset.const, [ca(v) for v in s.batch])
-        self.bmode = load_mode(s.b_rs, s.b_ks, s.N, s.K, s.lb.offset.const, [cb(v) for v in s.batch])
         self.followers = []             # (kernel, var map, forwarded loads) run in the epilogue
 
     def hoistable(self, stages):
@@ -292,6 +302,8 @@ class GemmPlan(Plan):
 
     def template_lds(self) -> int:
         """LDS of the anvil_mfma.h templates the kernel instantiates."""
+        if self.slab:
+            return 4 * (2 * 2 * self.slab * 33 + 4 * 16 * 64)
         if self.sched == "tile":
             return 2 * 4 * 16 * ((self.BM + 4) + (self.BN + 4))
         return self.waves * 16 * 64 * 4
@@ -363,7 +375,14 @@ class GemmPlan(Plan):
                     "        const int ni = n0 + (lane & 31);",
                     f"        if (mi >= {s.M} || ni >= {s.N}) continue;"]
             slot = "q"
-            if self.pipe:
+            if self.slab:
+                kargs = (f"pa, {s.a_rs}LL, {s.a_ks}LL, pb, {s.b_rs}LL, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, {s.K}, "
+                         "opa, opb")
+                chk = lambda n: "true" if n % 32 else "false"
+                main = [f"    float part[1][1][{per}];",
+                        f"    anvil_mm_tile_kslab<{self.amode}, {self.bmode}, {self.slab}, {chk(s.M)}, {chk(s.N)}>"
+                        f"(part, {kargs});"]
+            elif self.pipe:
                 kargs = (f"pa, {s.a_rs}LL, {s.a_ks}LL, pb, {s.b_rs}LL, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, {s.K}, "
                          "opa, opb")
                 chk = lambda n: "true" if n % 32 else "false"

@@ -362,4 +362,146 @@ __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W]
             }
 }
 
+// The K split with operands staged through LDS: the workgroup's 256 lanes load each KC-deep chunk
+// of A (32 rows) and B (32 columns) with 16-byte loads along whichever index is contiguous in
+// memory (a wavefront's load covers a few whole cache lines, where loading MFMA operands straight
+// into registers touches one line per row), store it to LDS k-major, and each wavefront runs the
+// MFMAs of its quarter of the chunk's k from LDS. The next chunk is loaded into registers while the
+// current one is multiplied; two LDS buffers, one barrier per chunk. The four partial tiles are
+// added through LDS in wave order at the end, as in anvil_mm_tile_ksplit.
+template <int MODE, int KC, bool CHKT, int LD>
+struct anvil_slab {
+    // one operand's 32 x KC chunk: element (t, k) at p[t * rs + k * ks]
+    static constexpr int PER = 32 * KC / 256;                       // elements per lane
+    float r[PER];
+
+    template <class OP>
+    __device__ __forceinline__ void load(const float *__restrict__ p, long long rs, long long ks, int t0, int tmax,
+                                         int k0, int kend, OP op, int tid) {
+        if (MODE == ANVIL_LD_KC) {                                  // 16 bytes along k
+#pragma unroll
+            for (int q = 0; q < PER / 4; q++) {
+                const int idx = tid + 256 * q, tl = idx / (KC / 4), kl = (idx % (KC / 4)) * 4;
+                const int t = t0 + tl, k = k0 + kl;
+                anvil_f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                if ((!CHKT || t < tmax) && k + 3 < kend) {
+                    v = *(const anvil_f32x4 *)(p + (long long)t * rs + k);
+                } else if (!CHKT || t < tmax) {
+                    if (k + 0 < kend) v.x = p[(long long)t * rs + k + 0];
+                    if (k + 1 < kend) v.y = p[(long long)t * rs + k + 1];
+                    if (k + 2 < kend) v.z = p[(long long)t * rs + k + 2];
+                }
+                r[4 * q + 0] = op(v.x);
+                r[4 * q + 1] = op(v.y);
+                r[4 * q + 2] = op(v.z);
+                r[4 * q + 3] = op(v.w);
+            }
+        } else if (MODE == ANVIL_LD_RC) {                           // 16 bytes along the tile index
+#pragma unroll
+            for (int q = 0; q < PER / 4; q++) {
+                const int idx = tid + 256 * q, kl = idx / 8, tl = (idx % 8) * 4;
+                const int t = t0 + tl, k = k0 + kl;
+                anvil_f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                if (k < kend) {
+                    if (!CHKT || t + 3 < tmax) {
+                        v = *(const anvil_f32x4 *)(p + (long long)k * ks + t);
+                    } else {
+                        if (t + 0 < tmax) v.x = p[(long long)k * ks + t + 0];
+                        if (t + 1 < tmax) v.y = p[(long long)k * ks + t + 1];
+                        if (t + 2 < tmax) v.z = p[(long long)k * ks + t + 2];
+                    }
+                }
+                r[4 * q + 0] = op(v.x);
+                r[4 * q + 1] = op(v.y);
+                r[4 * q + 2] = op(v.z);
+                r[4 * q + 3] = op(v.w);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < PER; q++) {
+                const int idx = tid + 256 * q, tl = idx % 32, kl = idx / 32;
+                const int t = t0 + tl, k = k0 + kl;
+                r[q] = ((!CHKT || t < tmax) && k < kend) ? op(p[(long long)t * rs + (long long)k * ks]) : 0.f;
+            }
+        }
+    }
+
+    // k-major in LDS: s[k * LD + t]
+    __device__ __forceinline__ void store(float *__restrict__ s, int tid) const {
+        if (MODE == ANVIL_LD_KC) {
+#pragma unroll
+            for (int q = 0; q < PER / 4; q++) {
+                const int idx = tid + 256 * q, tl = idx / (KC / 4), kl = (idx % (KC / 4)) * 4;
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[(kl + i) * LD + tl] = r[4 * q + i];
+            }
+        } else if (MODE == ANVIL_LD_RC) {
+#pragma unroll
+            for (int q = 0; q < PER / 4; q++) {
+                const int idx = tid + 256 * q, kl = idx / 8, tl = (idx % 8) * 4;
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[kl * LD + tl + i] = r[4 * q + i];
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < PER; q++) {
+                const int idx = tid + 256 * q, tl = idx % 32, kl = idx / 32;
+                s[kl * LD + tl] = r[q];
+            }
+        }
+    }
+};
+
+template <int AMODE, int BMODE, int KC, bool CHKM, bool CHKN, class OPA, class OPB>
+__device__ __forceinline__ void anvil_mm_tile_kslab(float (&out)[1][1][4],
+                                                    const float *__restrict__ a, long long a_rs, long long a_ks,
+                                                    const float *__restrict__ b, long long b_rs, long long b_ks,
+                                                    int M, int N, int m0, int n0, int K, OPA opa, OPB opb) {
+    constexpr int LD = 33;                                          // odd: k-major stores spread over banks
+    __shared__ float As[2][KC * LD];
+    __shared__ float Bs[2][KC * LD];
+    __shared__ float part[4 * 16 * 64];
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    anvil_slab<AMODE, KC, CHKM, LD> sa;
+    anvil_slab<BMODE, KC, CHKN, LD> sb;
+    anvil_mm_acc<1, 1> acc;
+    acc.zero();
+    sa.load(a, a_rs, a_ks, m0, M, 0, K, opa, tid);
+    sb.load(b, b_rs, b_ks, n0, N, 0, K, opb, tid);
+    sa.store(As[0], tid);
+    sb.store(Bs[0], tid);
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 < K; k0 += KC) {
+        const int next = k0 + KC;
+        if (next < K) {
+            sa.load(a, a_rs, a_ks, m0, M, next, K, opa, tid);
+            sb.load(b, b_rs, b_ks, n0, N, next, K, opb, tid);
+        }
+        const float *as = As[buf] + (KC / 4) * w * LD;
+        const float *bs = Bs[buf] + (KC / 4) * w * LD;
+#pragma unroll
+        for (int kk = 0; kk < KC / 4; kk += 2)
+            acc.c[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(as[(kk + h) * LD + r], bs[(kk + h) * LD + r],
+                                                               acc.c[0][0], 0, 0, 0);
+        if (next < K) {
+            sa.store(As[buf ^ 1], tid);
+            sb.store(Bs[buf ^ 1], tid);
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+#pragma unroll
+    for (int v = 0; v < 16; v++) part[(w * 16 + v) * 64 + lane] = acc.c[0][0][v];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        float s = 0.f;
+#pragma unroll
+        for (int src = 0; src < 4; src++) s += part[(src * 16 + 4 * w + q) * 64 + lane];
+        out[0][0][q] = s;
+    }
+}
+
 #endif
