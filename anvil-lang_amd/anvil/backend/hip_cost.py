@@ -56,8 +56,22 @@ def kernel_bytes(k: ir.Kernel) -> int:
 
 
 def plan_cost(plan) -> tuple[int, int]:
-    """(FLOPs, bytes) of one launch of a generated kernel."""
-    flops = sum(kernel_flops(k) for k in plan.kernels)
+    """(FLOPs, bytes) of one launch of a generated kernel. A matrix product counts 2·M·N·K (per batch)
+    for its contraction, the matrix-core work, whatever scale factors the IR multiplies inside the
+    sum (they are applied once per output); launches of several kernels side by side add up."""
+    if plan.kind == "fused":
+        fl = by = 0
+        for p in plan.parts:
+            f, b = plan_cost(p)
+            fl, by = fl + f, by + b
+        return fl, by
+    if plan.kind == "gemm":
+        s = plan.s
+        flops = 2 * s.M * s.N * s.K * s.B + sum(kernel_flops(k) for k in plan.kernels[1:])
+        flops += ir.prod(v.extent for v in plan.kernels[0].domain) * sum(expr_ops(st.value)
+                                                                         for st in plan.kernels[0].stmts)
+    else:
+        flops = sum(kernel_flops(k) for k in plan.kernels)
     written: set = set()
     reach: dict = {}
     out_bytes = 0
