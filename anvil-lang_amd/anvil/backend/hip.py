@@ -108,6 +108,9 @@ class HipGen:
                  graphs: bool = False):
         if not emulate and os.environ.get("ANVIL_HIP_SINK", "1") != "0":
             prog = A.sink_scalar_kernels(prog)
+        if not emulate and os.environ.get("ANVIL_HIP_GATHER_FWD", "1") != "0":
+            from . import hip_gemm
+            prog = hip_gemm.forward_gather_copies(prog, A.host_scalars(prog))
         self.prog = prog
         self.seed = seed & 0xFFFFFFFF
         self.library = library
@@ -297,11 +300,20 @@ class HipGen:
         self.mark_dead_stores(plan)
         return plan, j - i
 
+    def exit_if(self, st) -> bool:
+        """An `if` on a host scalar whose only effect is to leave the loop (or iteration)."""
+        return (isinstance(st, ir.If) and st.cond.root.id in self.hosts and not st.orelse.stmts
+                and len(st.then.stmts) == 1 and isinstance(st.then.stmts[0], (ir.Break, ir.Continue)))
+
     def side_by_side(self, stmts, i, plan, used):
         """Join the launches after `plan` that are independent of it (and of each other) into one
         FusedPlan. Host scalar kernels between them then run before the launch: only if no part
         before them reads what they write. Parts must agree on the workgroup size (a split kernel
-        is re-planned to it) unless they have no barrier; their LDS adds up."""
+        is re-planned to it) unless they have no barrier; their LDS adds up.
+
+        The scan may cross one `if (host scalar) break;` (a step limit checked after the batch is
+        gathered): the launch then goes after the check, and the leaving path launches the parts
+        that came before the check on their own, so they run exactly when they did."""
         if self.emulate or os.environ.get("ANVIL_HIP_SIDE", "1") == "0":
             return plan, used
         ids = lambda bs: {b.root.id for b in bs}
@@ -316,12 +328,21 @@ class HipGen:
         hoisted = list(getattr(plan, "hoisted", []))
         reads, writes = rw(plan)
         threads = plan.grid()[1]
-        lds = HK.lds_bytes(plan)
         j = i + used
         taken = used
         between: list = []
-        while j < len(stmts) and isinstance(stmts[j], KernelStmt) and len(parts) < 8:
-            k = stmts[j].kernel
+        exit_at = None      # (the if, parts before it, host kernels hoisted before it, the ones after it)
+        while j < len(stmts) and len(parts) < 8:
+            st = stmts[j]
+            if (exit_at is None and not self.graphs and self.exit_if(st)
+                    and os.environ.get("ANVIL_HIP_EXIT", "1") != "0"):
+                exit_at = (st, len(parts), list(hoisted), list(between))
+                between = []
+                j += 1
+                continue
+            if not isinstance(st, KernelStmt):
+                break
+            k = st.kernel
             if A.is_host_kernel(k, self.hosts):
                 between.append(k)
                 j += 1
@@ -330,7 +351,7 @@ class HipGen:
             if cand.kind in ("serial", "fused"):
                 break
             moved = between + list(getattr(cand, "hoisted", []))
-            if {st.buf.root.id for h in moved for st in h.stores} & reads:
+            if {st2.buf.root.id for h in moved for st2 in h.stores} & reads:
                 break
             cr, cw = rw(cand)
             if cw & (reads | writes) or cr & writes:
@@ -357,9 +378,21 @@ class HipGen:
             writes |= cw
             j += cused
             taken = j - i
+        if exit_at is not None and len(parts) == exit_at[1]:
+            hoisted = exit_at[2]                        # nothing joined past the check: stop before it
+            exit_at = None
         if len(parts) == 1:
             return plan, used
-        return HK.FusedPlan(self, parts, "f" + plan.name, hoisted), taken
+        if exit_at is None:
+            return HK.FusedPlan(self, parts, "f" + plan.name, hoisted), taken
+        st, n_pre, before, pre_hosts = exit_at
+        pre = parts[:n_pre]
+        pre_plan = pre[0] if len(pre) == 1 else HK.FusedPlan(self, pre, "e" + plan.name, [])
+        pre_hoist = before + pre_hosts
+        post_hoist = hoisted[len(before):]
+        fused = HK.FusedPlan(self, parts, "f" + plan.name, pre_hoist + post_hoist)
+        fused.exit = (st, pre_plan, pre_hoist, post_hoist)
+        return fused, taken
 
     def absorb_followers(self, plan, stmts, j) -> int:
         """Elementwise kernels right after a product (past host-only scalar kernels, which are then
@@ -469,6 +502,8 @@ class HipGen:
                 if plan is None:
                     plan, used = self.plan_run(stmts, i)
                     plan, used = self.side_by_side(stmts, i, plan, used)
+                    if getattr(plan, "exit", None) is not None:
+                        self.plans.append(plan.exit[1])
                     self.plans.append(plan)
                     self.plan_of[k.id] = (plan, used)
                     for part in getattr(plan, "parts", [plan]):
@@ -477,11 +512,24 @@ class HipGen:
                             self.part_of[kk.id] = part
                 else:
                     plan, used = plan
-                for hk in getattr(plan, "hoisted", []):
-                    seg.append(("host", self.host_kernel(hk, ind), None))
-                    twin = self.twin_of(hk)
-                    if twin is not None:
-                        seg.append(("twin", self.launch(twin, ind), twin))
+                exit_ = getattr(plan, "exit", None)
+                if exit_ is not None:
+                    # the host's scalar kernels before the check, the check (whose leaving path
+                    # launches what came before it), the ones after it, then the whole launch
+                    st_if, pre_plan, pre_hoist, post_hoist = exit_
+                    for hk in pre_hoist:
+                        seg.append(("host", self.host_kernel(hk, ind), None))
+                    leave = "break;" if isinstance(st_if.then.stmts[0], ir.Break) else "continue;"
+                    seg.append(("host", [f"{ind}if ({self.scalar_value(st_if.cond)} != 0) {{"]
+                                + self.launch(pre_plan, ind + "    ") + [f"{ind}    {leave}", f"{ind}}}"], None))
+                    for hk in post_hoist:
+                        seg.append(("host", self.host_kernel(hk, ind), None))
+                else:
+                    for hk in getattr(plan, "hoisted", []):
+                        seg.append(("host", self.host_kernel(hk, ind), None))
+                        twin = self.twin_of(hk)
+                        if twin is not None:
+                            seg.append(("twin", self.launch(twin, ind), twin))
                 seg.append(("launch", self.launch(plan, ind), plan))
                 i += used
                 continue

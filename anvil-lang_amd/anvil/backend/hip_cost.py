@@ -45,8 +45,23 @@ def kernel_reach(k: ir.Kernel) -> dict:
             b = ld.buf.root
             if not b.shape:
                 continue                                # a scalar argument
-            reach[b] = reach.get(b, 0) + n
+            reach[b] = reach.get(b, 0) + min(n, _distinct(ld.offset))
     return reach
+
+
+def _distinct(off: ir.Affine) -> int:
+    """At most how many different elements an offset addresses: the product of the extents of the
+    loop variables it depends on (through gathered indices too)."""
+    vs: dict = {}
+
+    def walk(a):
+        for t in a.terms:
+            if isinstance(t, ir.Var):
+                vs[t.id] = t.extent or 1
+            elif isinstance(t, ir.Gather):
+                walk(t.load.offset)
+    walk(off)
+    return ir.prod(vs.values())
 
 
 def kernel_bytes(k: ir.Kernel) -> int:

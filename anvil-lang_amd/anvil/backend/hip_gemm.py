@@ -18,7 +18,7 @@ from __future__ import annotations
 import os
 
 from .. import ir
-from ..ir import F32, Binary, Const, Load, Unary, Var
+from ..ir import F32, Binary, Const, KernelStmt, Load, Unary, Var
 from . import hip_analysis as A
 from .hip_emit import Emitter, flit
 from .hip_kernels import KernelScope, Plan, canon_key, decode
@@ -43,6 +43,37 @@ def _const_value(e):
     return None
 
 
+def gathered_row(ld):
+    """(gather, its coefficient, the variable it is indexed by) when ld's offset is c·G + (terms in
+    other loop variables), G = idx[v + scalars + const] a checked gather: an operand whose rows are
+    picked through an index array (a shuffled batch). None otherwise."""
+    gs = ld.offset.gathers()
+    if len(gs) != 1 or gs[0].rest is not None:
+        return None
+    g = gs[0]
+    c = ld.offset.terms[g]
+    inner = g.load.offset
+    vs = [t for t in inner.terms if isinstance(t, Var)]
+    if c <= 0 or len(vs) != 1 or inner.terms[vs[0]] != 1 or inner.gathers():
+        return None
+    if any(not isinstance(t, (Var, ir.ScalarRef)) for t in inner.terms):
+        return None
+    v = vs[0]
+    if any(not isinstance(t, Var) for t in ld.offset.terms if t is not g) or ld.offset.coef(v):
+        return None
+    return g, c, v
+
+
+def _coef_fn(ld):
+    """Coefficient of each loop variable in an operand's offset; a gathered row counts its gather's
+    coefficient for the variable that indexes it."""
+    gr = gathered_row(ld)
+    if gr is None:
+        return ld.offset.coef
+    _, c, gv = gr
+    return lambda v: c if v is gv else ld.offset.coef(v)
+
+
 def _single_load(e):
     """The one array load of an elementwise operand expression (other leaves constants), or None."""
     loads = []
@@ -51,10 +82,11 @@ def _single_load(e):
             loads.append(x)
         elif not isinstance(x, (Const, Unary, Binary, Load)):
             return None
+    loads = [x for x in loads if not any(x is g.load for y in loads for g in y.offset.gathers())]
     if len(loads) != 1 or not loads[0].buf.root.shape or loads[0].buf.dtype != F32:
         return None
     ld = loads[0]
-    if any(not isinstance(t, Var) for t in ld.offset.terms):
+    if any(not isinstance(t, Var) for t in ld.offset.terms) and gathered_row(ld) is None:
         return None
     return ld
 
@@ -102,7 +134,7 @@ def analyse(k: ir.Kernel):
     dom, rv = list(k.domain), list(red.vars)
     best = None
     for (ea, la), (eb, lb) in (((ops[0], lds[0]), (ops[1], lds[1])), ((ops[1], lds[1]), (ops[0], lds[0]))):
-        ca, cb = la.offset.coef, lb.offset.coef
+        ca, cb = _coef_fn(la), _coef_fn(lb)
         if any(not ca(v) or not cb(v) for v in rv):
             continue
         mv = [v for v in dom if ca(v) and not cb(v)]
@@ -135,6 +167,10 @@ def analyse(k: ir.Kernel):
         s.N = ir.prod(v.extent for v in s.n_vars)
         s.K = ir.prod(v.extent for v in s.k_vars)
         s.B = ir.prod(v.extent for v in s.batch)
+        s.a_gather, s.b_gather = gathered_row(la), gathered_row(lb)
+        if (s.a_gather and (s.m_vars != [s.a_gather[2]] or s.batch or any(ca(v) for v in nv))) or \
+                (s.b_gather and (s.n_vars != [s.b_gather[2]] or s.batch or any(cb(v) for v in mv))):
+            continue                                    # rows picked through an index: one plain row variable
         # prefer the assignment whose n is the output's innermost (contiguous) variable
         score = 1 if dom[-1] in s.n_vars else 0
         if best is None or score > best[0]:
@@ -151,13 +187,143 @@ def load_mode(rs, ks, T, K, const, batch_strides):
     return "ANVIL_LD_ANY"
 
 
+def gathered_ok(s) -> bool:
+    """Operands with gathered rows are supported by the pipelined K split only, loading 16 bytes
+    along k from each row (so K a multiple of 8, rows starting on 16 bytes)."""
+    for g, rs, ks, T in ((s.a_gather, s.a_rs, s.a_ks, s.M), (s.b_gather, s.b_rs, s.b_ks, s.N)):
+        if g is not None and (s.K % 8 or ks != 1 or g[1] % 4 or os.environ.get("ANVIL_GEMM_PIPE", "1") == "0"):
+            return False
+    return True
+
+
 def match(gen, k: ir.Kernel, name: str):
     if gen.emulate or any(st.accumulate for st in k.stores):
         return None
     s = analyse(k)
-    if s is None or s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < MIN_SIDE:
+    if s is None or s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < MIN_SIDE or not gathered_ok(s):
         return None
     return GemmPlan(gen, k, name, s)
+
+
+def forward_gather_copies(prog: ir.Program, hosts: set) -> ir.Program:
+    """A kernel that only copies rows picked through an index array into a batch buffer
+    (xb[i, j] = X[perm[s·B + i], j]) and a later product that reads the batch buffer: the product
+    reads X through the index instead (its operand rows are gathered as it loads them), so it no
+    longer waits for the copy, and the two can run side by side. The copy stays for the batch
+    buffer's other readers. Done only where the product then keeps its matrix-core schedule."""
+    import dataclasses
+    from . import hip_analysis as A
+
+    def copy_kernel(st):
+        if not isinstance(st, KernelStmt):
+            return None
+        k = st.kernel
+        if k.red is not None or len(k.stmts) != 1 or not isinstance(k.stmts[0], ir.Store) or not k.domain:
+            return None
+        store = k.stmts[0]
+        if store.accumulate or not isinstance(store.value, Load) or not A.parallel_safe(k):
+            return None
+        strides = ir.row_major_strides([v.extent for v in k.domain])
+        want = ir.Affine(0, {v: st_ for v, st_ in zip(k.domain, strides) if v.extent > 1})
+        if store.offset != want or store.buf.root.numel != ir.prod(v.extent for v in k.domain):
+            return None
+        if not store.value.offset.gathers():
+            return None
+        return k, store.buf.root, store.value, dict(zip(k.domain, strides))
+
+    def subst(off: ir.Affine, m: dict) -> ir.Affine:
+        out = ir.Affine(off.const)
+        for t, c in off.terms.items():
+            if isinstance(t, Var):
+                out = out + m.get(t, ir.Affine(0)) * c
+            elif isinstance(t, ir.Gather):
+                g = ir.Gather(Load(t.load.buf, subst(t.load.offset, m)), t.bound, t.where, None)
+                out = out + ir.Affine(0, {g: c})
+            else:
+                out = out + ir.Affine(0, {t: c})
+        return out
+
+    def rewrite(c: ir.Kernel, cp):
+        pk, dst, src, strides = cp
+        by_stride = {st_: v for v, st_ in strides.items() if v.extent > 1}
+        ok = [True]
+
+        def fn(e):
+            if not isinstance(e, Load) or e.buf.root is not dst:
+                return e
+            off = e.offset
+            if off.const or off.gathers() or off.scalars():
+                ok[0] = False
+                return e
+            m, used = {}, set()
+            for t, coef in off.terms.items():
+                v = by_stride.get(coef)
+                if v is None or v in used or t.extent > v.extent:
+                    ok[0] = False
+                    return e
+                used.add(v)
+                m[v] = ir.Affine(0, {t: 1})
+            return Load(src.buf, subst(src.offset, m))
+        if c.red is None:
+            return None
+        body = ir.map_expr(c.red.body, fn)
+        lets: dict = {}                                   # old Let -> its copy (LetRefs follow)
+
+        def fn2(e):
+            if isinstance(e, ir.LetRef) and id(e.let) in lets:
+                return ir.LetRef(lets[id(e.let)])
+            return fn(e)
+        stmts = []
+        for st in c.stmts:
+            new = dataclasses.replace(st, value=ir.map_expr(st.value, fn2))
+            if isinstance(st, ir.Let):
+                lets[id(st)] = new
+            stmts.append(new)
+        if not ok[0] or any(st.buf.root is dst for st in c.stores):
+            return None
+        k2 = dataclasses.replace(c, red=dataclasses.replace(c.red, body=body), stmts=stmts)
+        if any(ld.buf.root is dst for ld in A.kernel_loads(k2)):
+            return None                                   # still reads the batch buffer elsewhere
+        s = analyse(k2)
+        if s is None or not (s.a_gather or s.b_gather) or not gathered_ok(s):
+            return None
+        if s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < MIN_SIDE:
+            return None
+        return k2
+
+    def block(blk: ir.Block) -> ir.Block:
+        out = [stmt(st) for st in blk.stmts]
+        for i, st in enumerate(out):
+            cp = copy_kernel(st)
+            if cp is None:
+                continue
+            pk, dst, src, _ = cp
+            guard = {dst.id} | {x.id for x in A.kernel_reads(pk)}
+            for j in range(i + 1, len(out)):
+                s2 = out[j]
+                if (isinstance(s2, ir.If) and not s2.orelse.stmts and len(s2.then.stmts) == 1
+                        and isinstance(s2.then.stmts[0], (ir.Break, ir.Continue))):
+                    continue                              # leaves the loop; writes nothing
+                if not isinstance(s2, KernelStmt):
+                    break
+                c = s2.kernel
+                if dst.id in {x.id for x in A.kernel_reads(c)}:
+                    k2 = rewrite(c, cp)
+                    if k2 is not None:
+                        out[j] = dataclasses.replace(s2, kernel=k2)
+                if guard & {x.id for x in A.kernel_writes(out[j].kernel)}:
+                    break
+        return dataclasses.replace(blk, stmts=out)
+
+    def stmt(st):
+        if isinstance(st, ir.For):
+            return dataclasses.replace(st, body=block(st.body))
+        if isinstance(st, ir.While):
+            return dataclasses.replace(st, cond_block=block(st.cond_block), body=block(st.body))
+        if isinstance(st, ir.If):
+            return dataclasses.replace(st, then=block(st.then), orelse=block(st.orelse))
+        return st
+    return dataclasses.replace(prog, main=block(prog.main))
 
 
 def subst_affine(a: ir.Affine, m: dict):
@@ -269,6 +435,8 @@ class GemmPlan(Plan):
             else:
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.waves, self.unroll = int(parts[1]), int(parts[2])
+        if s.a_gather or s.b_gather:                    # gathered rows: the pipelined K split only
+            self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
         self.pipe = self.pipe and self.sched == "ksplit" and not self.slab
         nch = -(-(s.K // 8) // self.waves)                  # chunks per wave
         self.depth = max(1, min(int(os.environ.get("ANVIL_GEMM_DEPTH", "2" if nch <= 32 else "4")), nch))
@@ -316,6 +484,21 @@ class GemmPlan(Plan):
 
     def grid(self):
         return (self.tn, self.tm, self.s.B), self.threads
+
+    def row_fn(self, sc, name, gather, rs) -> str:
+        """A device lambda: where row t of an operand starts (t·rs, or c·idx[t + ...] for a gathered
+        row, with the gather's bounds check)."""
+        if gather is None:
+            return f"    auto {name} = [=](int t) -> long long {{ return (long long)t * {rs}LL; }};"
+        g, c, v = gather
+        lines: list[str] = []
+        em = Emitter(sc, lines, "        ", prefix=f"{name}_")
+        saved = dict(sc.names)
+        sc.names[v] = "t"
+        val = em.gather(g)
+        sc.names = saved
+        return "\n".join([f"    auto {name} = [=](int t) -> long long {{"] + lines +
+                         [f"        return {c}LL * (long long){val};", "    };"])
 
     def operand(self, sc, e, ld, name) -> str:
         """A device lambda applying the operand's elementwise function to a loaded value."""
@@ -383,7 +566,8 @@ class GemmPlan(Plan):
                         f"    anvil_mm_tile_kslab<{self.amode}, {self.bmode}, {self.slab}, {chk(s.M)}, {chk(s.N)}>"
                         f"(part, {kargs});"]
             elif self.pipe:
-                kargs = (f"pa, {s.a_rs}LL, {s.a_ks}LL, pb, {s.b_rs}LL, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, {s.K}, "
+                body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs), self.row_fn(sc, "brow", s.b_gather, s.b_rs)]
+                kargs = (f"pa, arow, {s.a_ks}LL, pb, brow, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, {s.K}, "
                          "opa, opb")
                 chk = lambda n: "true" if n % 32 else "false"
                 nch = -(-(s.K // 8) // W)

@@ -1110,7 +1110,7 @@ class FusedPlan(Plan):
             _, t = p.grid()
             head = f"__global__ void __launch_bounds__({t}) {p.name}("
             assert head in src, p.name
-            src = src.replace(head, f"__device__ __forceinline__ void {p.name}_part(const uint3 anvil_b, "
+            src = src.replace(head, f"__device__ __forceinline__ void {self.name}_{p.name}(const uint3 anvil_b, "
                                     f"const uint3 anvil_g, ", 1)
             src = src.replace("blockIdx.", "anvil_b.").replace("gridDim.", "anvil_g.")
             texts.append(src)
@@ -1119,7 +1119,7 @@ class FusedPlan(Plan):
             args = ", ".join(name for name, _ in self.part_params(j, p))
             guard = "" if t == self.threads else f"if (threadIdx.x < {t}u) "
             calls += [f"    if (b < {n}u) {{",
-                      f"        {guard}{p.name}_part(make_uint3(b % {gx}u, b / {gx}u % {gy}u, b / {gx * gy}u), "
+                      f"        {guard}{self.name}_{p.name}(make_uint3(b % {gx}u, b / {gx}u % {gy}u, b / {gx * gy}u), "
                       f"make_uint3({gx}u, {gy}u, {gz}u), {args});",
                       "        return;",
                       "    }",

@@ -268,30 +268,32 @@ __device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][16 / W
 // reuses those registers for the chunk D ahead, so the matrix cores start on the first data to
 // arrive instead of after the last. The chunk loop is unrolled (NCH is a compile-time constant):
 // straight-line code, where the compiler's wait counts are exact. Rows and columns past M / N are
-// zero (CHKM, CHKN: the tile may cross the edge); k is always in range.
+// zero (CHKM, CHKN: the tile may cross the edge); k is always in range. Where row (column) t of
+// an operand starts is arow(t) (brow(t)): t times its stride, or, for rows picked through an index
+// array (a shuffled batch, X[perm[i]]), that row's offset; each lane computes its rows' once.
 template <int MODE, bool CHK>
-__device__ __forceinline__ void anvil_chunk_load_k(float (&r)[4], const float *__restrict__ p, long long rs, long long ks,
+__device__ __forceinline__ void anvil_chunk_load_k(float (&r)[4], const float *__restrict__ p, long long toff, long long ks,
                                                    int t, int tmax, int k) {
     if (CHK && t >= tmax) {
         r[0] = r[1] = r[2] = r[3] = 0.f;
         return;
     }
     if (MODE == ANVIL_LD_KC) {
-        const anvil_f32x4 v = *(const anvil_f32x4 *)(p + (long long)t * rs + k);
+        const anvil_f32x4 v = *(const anvil_f32x4 *)(p + toff + k);
         r[0] = v.x;
         r[1] = v.y;
         r[2] = v.z;
         r[3] = v.w;
     } else {
 #pragma unroll
-        for (int s = 0; s < 4; s++) r[s] = p[(long long)t * rs + (long long)(k + s) * ks];
+        for (int s = 0; s < 4; s++) r[s] = p[toff + (long long)(k + s) * ks];
     }
 }
 
 template <int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, bool FULL, class OPA, class OPB>
 __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
-                                                    const float *__restrict__ a, long long a_rs, long long a_ks,
-                                                    const float *__restrict__ b, long long b_rs, long long b_ks,
+                                                    const float *__restrict__ a, const long long (&ao)[TM], long long a_ks,
+                                                    const float *__restrict__ b, const long long (&bo)[TN], long long b_ks,
                                                     int M, int N, int m0, int n0, int c0, int n, OPA opa, OPB opb) {
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     float ab[D][TM][4], bb[D][TN][4];
@@ -299,9 +301,9 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
     if (FULL || (c) < n) {                                                                                 \
         const int k_ = 8 * (c0 + (c)) + 4 * h;                                                             \
         _Pragma("unroll") for (int i = 0; i < TM; i++)                                                     \
-            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, a_rs, a_ks, m0 + 32 * i + r, M, k_);             \
+            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, ao[i], a_ks, m0 + 32 * i + r, M, k_);            \
         _Pragma("unroll") for (int j = 0; j < TN; j++)                                                     \
-            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, b_rs, b_ks, n0 + 32 * j + r, N, k_);             \
+            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, bo[j], b_ks, n0 + 32 * j + r, N, k_);            \
     }
 #pragma unroll
     for (int c = 0; c < D; c++) ANVIL_KP_LOAD(c, c)
@@ -324,23 +326,29 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
 #undef ANVIL_KP_LOAD
 }
 
-template <int W, int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, class OPA, class OPB>
+template <int W, int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, class AROW, class BROW,
+          class OPA, class OPB>
 __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W],
-                                                    const float *__restrict__ a, long long a_rs, long long a_ks,
-                                                    const float *__restrict__ b, long long b_rs, long long b_ks,
+                                                    const float *__restrict__ a, AROW arow, long long a_ks,
+                                                    const float *__restrict__ b, BROW brow, long long b_ks,
                                                     int M, int N, int m0, int n0, int K, OPA opa, OPB opb) {
     constexpr int PER = 16 / W;
     __shared__ float part[W * TM * TN * 16 * 64];
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, r = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     // uniform: scalar branches
     const int c0 = w * NCH, n = min(NCH, max(0, (K >> 3) - c0));
+    long long ao[TM], bo[TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) ao[i] = (!CHKM || m0 + 32 * i + r < M) ? arow(m0 + 32 * i + r) : 0;
+#pragma unroll
+    for (int j = 0; j < TN; j++) bo[j] = (!CHKN || n0 + 32 * j + r < N) ? brow(n0 + 32 * j + r) : 0;
     anvil_mm_acc<TM, TN> acc;
     acc.zero();
     if (n == NCH)
-        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, true>(acc, a, a_rs, a_ks, b, b_rs, b_ks, M, N,
+        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, true>(acc, a, ao, a_ks, b, bo, b_ks, M, N,
                                                                             m0, n0, c0, n, opa, opb);
     else if (n > 0)
-        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, false>(acc, a, a_rs, a_ks, b, b_rs, b_ks, M, N,
+        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, false>(acc, a, ao, a_ks, b, bo, b_ks, M, N,
                                                                              m0, n0, c0, n, opa, opb);
 #pragma unroll
     for (int i = 0; i < TM; i++)
