@@ -232,6 +232,11 @@ class HipGen:
     # ------------------------------------------------------------------ planning kernels
     def plan_run(self, stmts: list, i: int):
         """The plan for the kernel at stmts[i] and how many statements it takes."""
+        if not self.emulate and os.environ.get("ANVIL_HIP_ATTN", "1") != "0":
+            from . import hip_attn
+            at = hip_attn.match(self, stmts, i)
+            if at is not None:
+                return at, 6
         got = self.row_block(stmts, i)
         if got is not None:
             return got

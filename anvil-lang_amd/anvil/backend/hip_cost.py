@@ -80,6 +80,9 @@ def plan_cost(plan) -> tuple[int, int]:
             f, b = plan_cost(p)
             fl, by = fl + f, by + b
         return fl, by
+    if plan.kind == "attention":                        # the two products; scores never stored
+        return 4 * plan.B * plan.Lq * plan.Lk * plan.D, 4 * (plan.Q.numel + plan.K.numel + plan.V.numel +
+                                                             plan.O.numel)
     if plan.kind == "gemm":
         s = plan.s
         flops = 2 * s.M * s.N * s.K * s.B + sum(kernel_flops(k) for k in plan.kernels[1:])

@@ -512,4 +512,131 @@ __device__ __forceinline__ void anvil_mm_tile_kslab(float (&out)[1][1][4],
     }
 }
 
+// Attention without the score matrix: O[b] = softmax(scale · Q[b] K[b]ᵀ) V[b], rows of Q in 32-query
+// tiles, one tile per workgroup whose four wavefronts each take a quarter of the keys (32 at a time)
+// and are merged at the end. Everything is computed transposed, Sᵀ = K Qᵀ and Oᵀ = Vᵀ Pᵀ, so that
+// lane l always holds query l % 32 (half h = l / 32): its running max and sum are lane-local, and
+// the Sᵀ accumulators of lane l (keys 8(v/4) + 4h + v%4 of the tile) are exactly the Pᵀ operand
+// lane l must supply to the next MFMAs, taking key slot h of MFMA v; the Vᵀ operand follows the same
+// key order. Output rows d of the DT = D/32 Oᵀ tiles are interleaved, d = DT·i + j, so each lane
+// loads DT consecutive floats of a V row at once. Per key tile: running max m, p = 2^(s - m) with s
+// in base 2 (Q pre-scaled by scale · log2 e), l = l·c + Σp, O = O·c + Vᵀ p with c = 2^(m_old - m_new)
+// (the online softmax; the reference exponentiates s·scale - max in base e after the full row: the
+// same values up to rounding). O is rescaled only when some lane's maximum moved. Q stays in registers (D/2 floats per
+// lane); the next tile's K and V rows are loaded while the current one is multiplied.
+template <int D>
+struct anvil_vec_of { typedef float type; };
+template <> struct anvil_vec_of<64> { typedef float __attribute__((ext_vector_type(2))) type; };
+template <> struct anvil_vec_of<128> { typedef anvil_f32x4 type; };
+
+template <int D>
+__device__ __forceinline__ void anvil_attention_tile(const float *__restrict__ q, const float *__restrict__ k,
+                                                     const float *__restrict__ v, float *__restrict__ o,
+                                                     float scale, int Lq, int Lk, int q0) {
+    constexpr int DH = D / 2;                  // k-dimension per lane half in Sᵀ = K Qᵀ
+    constexpr int DT = D / 32;                 // Oᵀ tiles
+    typedef typename anvil_vec_of<D>::type vec;
+    __shared__ float part[4][DT][16][64];
+    __shared__ float stat[4][2][32];
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int per = Lk / 4, kb = w * per;
+    // scores in base 2: Q is scaled once by scale · log2(e), and p = 2^(s - m) (v_exp_f32)
+    const float qs = scale * 1.4426950408889634f;
+    float qr[DH];
+#pragma unroll
+    for (int s4 = 0; s4 < DH; s4 += 4) {
+        const anvil_f32x4 x = *(const anvil_f32x4 *)(q + (long long)(q0 + r) * D + DH * h + s4);
+        qr[s4] = x.x * qs; qr[s4 + 1] = x.y * qs; qr[s4 + 2] = x.z * qs; qr[s4 + 3] = x.w * qs;
+    }
+    anvil_f32x16 oacc[DT];
+#pragma unroll
+    for (int j = 0; j < DT; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) oacc[j][e] = 0.f;
+    float m = -__builtin_inff(), l = 0.f;
+    float kr[DH];
+    vec vr[16];
+#define ANVIL_AT_LOADK(K0)                                                                                 \
+    _Pragma("unroll") for (int s4 = 0; s4 < DH; s4 += 4) {                                                 \
+        const anvil_f32x4 x = *(const anvil_f32x4 *)(k + (long long)((K0) + r) * D + DH * h + s4);          \
+        kr[s4] = x.x; kr[s4 + 1] = x.y; kr[s4 + 2] = x.z; kr[s4 + 3] = x.w;                                 \
+    }
+#define ANVIL_AT_LOADV(K0)                                                                                 \
+    _Pragma("unroll") for (int t = 0; t < 16; t++)                                                         \
+        vr[t] = *(const vec *)(v + (long long)((K0) + 8 * (t >> 2) + 4 * h + (t & 3)) * D + DT * r);
+    ANVIL_AT_LOADK(kb)
+    ANVIL_AT_LOADV(kb)
+    for (int k0 = kb; k0 < kb + per; k0 += 32) {
+        anvil_f32x16 sacc;
+#pragma unroll
+        for (int e = 0; e < 16; e++) sacc[e] = 0.f;
+#pragma unroll
+        for (int s = 0; s < DH; s++) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[s], qr[s], sacc, 0, 0, 0);
+        if (k0 + 32 < kb + per) ANVIL_AT_LOADK(k0 + 32)
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int e = 0; e < 16; e++) mx = fmaxf(mx, sacc[e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);
+        const float c = (mn == -__builtin_inff()) ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+        float ps = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            sacc[e] = __builtin_amdgcn_exp2f(sacc[e] - mn);
+            ps += sacc[e];
+        }
+        ps += __shfl_xor(ps, 32, 64);
+        l = l * c + ps;
+        m = mn;
+        if (!__all(c == 1.f)) {                 // a new maximum somewhere in the wave: rescale O
+#pragma unroll
+            for (int j = 0; j < DT; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) oacc[j][e] *= c;
+        }
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const float *vt = (const float *)&vr[t];
+#pragma unroll
+            for (int j = 0; j < DT; j++) oacc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[j], sacc[t], oacc[j], 0, 0, 0);
+        }
+        if (k0 + 32 < kb + per) ANVIL_AT_LOADV(k0 + 32)
+    }
+#undef ANVIL_AT_LOADK
+#undef ANVIL_AT_LOADV
+    // merge the four waves' (m, l, O) for each query, wave j finishing Oᵀ tile j (DT <= 4 ... DT tiles
+    // split over the waves)
+    if (h == 0) {
+        stat[w][0][r] = m;
+        stat[w][1][r] = l;
+    }
+#pragma unroll
+    for (int j = 0; j < DT; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) part[w][j][e][lane] = oacc[j][e];
+    __syncthreads();
+    float M = stat[0][0][r];
+#pragma unroll
+    for (int x = 1; x < 4; x++) M = fmaxf(M, stat[x][0][r]);
+    float f[4], L = 0.f;
+#pragma unroll
+    for (int x = 0; x < 4; x++) {
+        const float mx = stat[x][0][r];
+        f[x] = (mx == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(mx - M);
+        L += f[x] * stat[x][1][r];
+    }
+    const float inv = 1.f / L;
+    for (int j = w; j < DT; j += 4) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int x = 0; x < 4; x++) acc += f[x] * part[x][j][e][lane];
+            const int row = 8 * (e >> 2) + 4 * h + (e & 3);          // Oᵀ row of tile j: d = DT·row + j
+            o[(long long)(q0 + r) * D + DT * row + j] = acc * inv;
+        }
+    }
+}
+
 #endif

@@ -434,6 +434,11 @@ PROGRAMS = [
      "function": {"name": "linear", "args": [([96, 80], "f32"), ([72, 80], "f32"), ([72], "f32")]}},
     {"name": "c3_attention_small", "source": C3_ATTENTION, "interp": True,
      "function": {"name": "attention", "args": [([2, 64, 32], "f32")] * 3}},
+    # shapes the one-kernel attention takes (head size 64 and 128, keys a multiple of 128)
+    {"name": "c3_attention_d64", "source": C3_ATTENTION, "interp": True,
+     "function": {"name": "attention", "args": [([2, 128, 64], "f32")] * 3}},
+    {"name": "c3_attention_d128", "source": C3_ATTENTION, "interp": True,
+     "function": {"name": "attention", "args": [([2, 256, 128], "f32")] * 3}},
     # the reference's CUDA backend test cases as programs
     {"name": "hello", "source": HELLO, "interp": True},
     {"name": "linreg", "source": LINREG, "interp": True, "keep": ["w", "b"]},

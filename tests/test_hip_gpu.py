@@ -38,6 +38,28 @@ def test_gpu_function_matches_reference(name):
         np.testing.assert_allclose(g, w, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(w))))
 
 
+def test_gpu_attention_at_full_size_matches_closed_form():
+    """C3's attention, Q, K, V [4, 2048, 128]: the one-kernel path (scores never stored) against
+    softmax(Q Kᵀ / √128) V computed in float64."""
+    print("gpu attention full size", flush=True)
+    from anvil.hip_function import Compiled, Lowered
+    prog, data = load_ir("c3_attention")
+    assert any("attention:" in line for line in _source_lines(prog, data)), "not the one-kernel schedule"
+    low = Lowered.from_fixture(prog, data)
+    rng = np.random.default_rng(2)
+    q, k, v = (rng.standard_normal((4, 2048, 128)).astype(np.float32) for _ in range(3))
+    got = Compiled(low.name, low, seed=data.get("seed", 0)).call([q, k, v])
+    s = np.einsum("bid,bjd->bij", q.astype(np.float64), k.astype(np.float64)) / np.sqrt(128.0)
+    p = np.exp(s - s.max(axis=2, keepdims=True))
+    want = np.einsum("bij,bjd->bid", p / p.sum(axis=2, keepdims=True), v.astype(np.float64))
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
+
+
+def _source_lines(prog, data):
+    from anvil.backend import hip
+    return hip.generate(prog, seed=data.get("seed", 0), library=True).splitlines()
+
+
 def test_gpu_bounds_check_reports_the_value():
     rc, out, err, _ = run_program("bounds", emulate=False, timeout=120)
     assert rc == 1
