@@ -3,6 +3,7 @@
     python -m anvil hip   PROG.json [-o PROG.hip] [--seed N]     write the generated .hip file
     python -m anvil build PROG.json [-o PROG.so]  [--seed N]     compile it for gfx950
     python -m anvil run   PROG.json [--seed N] [--profile] [--dump OUT.npz --keep a,b,...]
+    python -m anvil export FN.json [-o DIR] [--name LIB]        a function as lib<LIB>.so + <LIB>.h
 
 These mirror the reference's `anvil cuda file.anvil` and `anvil run|build --cuda` (cli.py:259-270,
 305-320): the same generated-file / build / run split, libraries cached by the hash of their source
@@ -49,7 +50,17 @@ def main(argv=None) -> int:
             q.add_argument("--dump", default=None, help="write the final contents of --keep buffers here (.npz)")
             q.add_argument("--keep", default="", help="comma-separated buffer names (or #id) to dump")
             q.add_argument("--marks", default=None, help="record an event per iteration of loops with this counter")
+    q = sub.add_parser("export", help="a lowered function as a C library and header (lib<name>.so, <name>.h)")
+    q.add_argument("program", help="a lowered function (.json, anvil-ir/1 with a \"function\" entry)")
+    q.add_argument("-o", "--output", default=None, help="the directory to write to")
+    q.add_argument("--name", default=None, help="the library's name (default: the file's)")
+    q.add_argument("--seed", type=int, default=None)
     args = p.parse_args(argv)
+    if args.cmd == "export":
+        from .export_hip import export
+        for path in export(args.program, args.output, name=args.name, seed=args.seed):
+            print(path)
+        return 0
     from .backend import hip
     prog, data = _load_program(args.program)
     seed = args.seed if args.seed is not None else int(data.get("seed", 0))

@@ -63,7 +63,8 @@ def main(ref_root: str) -> None:
             prog = low.prog
             data = irjson.dump(prog)
             data["function"] = {"name": fn["name"], "inputs": [b.id for b in low.inputs],
-                                "outputs": [None if b is None else b.id for b in low.outputs]}
+                                "outputs": [None if b is None else b.id for b in low.outputs],
+                                "arg_names": list(low.arg_names), "out_names": list(low.out_names)}
         else:
             prog = compile_text(spec["source"], path=path, consts=spec.get("consts")).program
             data = irjson.dump(prog)
