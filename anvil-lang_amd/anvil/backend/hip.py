@@ -105,10 +105,15 @@ class HostScope(Scope):
 
 class HipGen:
     def __init__(self, prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False,
-                 graphs: bool = False):
-        if not emulate and os.environ.get("ANVIL_HIP_SINK", "1") != "0":
+                 graphs: bool = False, check: str | None = None):
+        # --check: one launch per IR kernel, in program order, each followed by a scan of what it
+        # wrote (no fusion, no reordering, no graphs: the first bad value is pinned to one kernel)
+        self.check = check
+        if check:
+            graphs = False
+        if not emulate and not check and os.environ.get("ANVIL_HIP_SINK", "1") != "0":
             prog = A.sink_scalar_kernels(prog)
-        if not emulate and os.environ.get("ANVIL_HIP_GATHER_FWD", "1") != "0":
+        if not emulate and not check and os.environ.get("ANVIL_HIP_GATHER_FWD", "1") != "0":
             from . import hip_gemm
             prog = hip_gemm.forward_gather_copies(prog, A.host_scalars(prog))
         self.prog = prog
@@ -232,6 +237,8 @@ class HipGen:
     # ------------------------------------------------------------------ planning kernels
     def plan_run(self, stmts: list, i: int):
         """The plan for the kernel at stmts[i] and how many statements it takes."""
+        if self.check:
+            return self.plan_one(stmts, i)
         if not self.emulate and os.environ.get("ANVIL_HIP_ATTN", "1") != "0":
             from . import hip_attn
             at = hip_attn.match(self, stmts, i)
@@ -288,7 +295,7 @@ class HipGen:
         if self.gemm is not None:
             g = self.gemm.match(self, k, name)
             if g is not None:
-                if os.environ.get("ANVIL_GEMM_FUSE", "1") == "0":      # tuning: no epilogue fusion
+                if os.environ.get("ANVIL_GEMM_FUSE", "1") == "0" or self.check:   # no epilogue fusion
                     return g, 1
                 return g, 1 + self.absorb_followers(g, stmts, i + 1)
         ty = HK.split_ways(k, self.emulate)
@@ -298,7 +305,8 @@ class HipGen:
             return HK.RowsPlan(self, [k], name, HK.rows_lanes(k, self.emulate), self.emulate), 1
         gb = HK.GroupBuilder(k)
         j = i + 1
-        while j < len(stmts) and isinstance(stmts[j], KernelStmt) and gb.fits(stmts[j].kernel, self.hosts):
+        while (not self.check and j < len(stmts) and isinstance(stmts[j], KernelStmt)
+               and gb.fits(stmts[j].kernel, self.hosts)):
             gb.add(stmts[j].kernel)
             j += 1
         plan = HK.RowsPlan(self, gb.kernels, name, HK.rows_lanes(k, self.emulate), self.emulate)
@@ -319,7 +327,7 @@ class HipGen:
         The scan may cross one `if (host scalar) break;` (a step limit checked after the batch is
         gathered): the launch then goes after the check, and the leaving path launches the parts
         that came before the check on their own, so they run exactly when they did."""
-        if self.emulate or os.environ.get("ANVIL_HIP_SIDE", "1") == "0":
+        if self.emulate or self.check or os.environ.get("ANVIL_HIP_SIDE", "1") == "0":
             return plan, used
         ids = lambda bs: {b.root.id for b in bs}
 
@@ -501,6 +509,8 @@ class HipGen:
                     twin = self.twin_of(k)
                     if twin is not None:
                         seg.append(("twin", self.launch(twin, ind), twin))
+                    if self.check:
+                        seg.append(("host", self.check_lines(k, ind), None))
                     i += 1
                     continue
                 plan = self.plan_of.get(k.id)
@@ -536,6 +546,9 @@ class HipGen:
                         if twin is not None:
                             seg.append(("twin", self.launch(twin, ind), twin))
                 seg.append(("launch", self.launch(plan, ind), plan))
+                if self.check:
+                    for kk in plan.kernels:
+                        seg.append(("host", self.check_lines(kk, ind), None))
                 i += used
                 continue
             flush(False)
@@ -546,6 +559,59 @@ class HipGen:
             out.extend(tail)
             self.tail_used = True
         return out
+
+    def check_lines(self, k: ir.Kernel, ind: str) -> list[str]:
+        """--check after kernel k: each f32 tensor it wrote (the caller's arrays aside), with the
+        tensors it read as the inputs the report counts nans and infinities in (aarch64.py:459-481)."""
+        written = []
+        for st in k.stores:
+            b = st.buf.root
+            if b.dtype == F32 and b.kind not in ir.EXTERN_KINDS and not getattr(b, "heap", False) and b not in written:
+                written.append(b)
+        if not written:
+            return []
+        reads: set = set()
+        for e in k.exprs():
+            for ld in ir.loads_in(e):
+                reads.add(ld.buf.root)
+        for st in k.stores:
+            if st.accumulate:
+                reads.add(st.buf.root)
+            for g in st.offset.gathers():
+                reads.add(g.load.buf.root)
+        inputs = [b for b in sorted(reads, key=lambda b: b.id)
+                  if b.dtype == F32 and b not in written and b.kind not in ir.EXTERN_KINDS
+                  and not getattr(b, "heap", False) and b.numel > 0]
+        desc = c_string(getattr(k, "desc", None) or self.describe(k))
+        mode = 2 if self.check == "inf" else 1
+
+        def where(b):
+            return (f"&anvil_h{b.id}", 1) if self.is_host(b) else (self.dev(b), 0)
+        out = []
+        for b in written:
+            name = f"`{b.name}` ({b.dtype}{list(b.shape)})" if b.shape else f"`{b.name}` (an f32 scalar)"
+            ptr, host = where(b)
+            ins = [f"{{{where(x)[0]}, {x.numel}LL, {where(x)[1]}, {c_string('`' + x.name + '`')}}}" for x in inputs]
+            dims = ", ".join(f"{d}LL" for d in b.shape) or "0LL"
+            out.append(f"{ind}{{   // --check {b.name}")
+            out.append(f"{ind}    static const long long dims_[] = {{{dims}}};")
+            out.append(f"{ind}    static const anvil_check_input ins_[] = {{{', '.join(ins) or '{NULL, 0LL, 0, NULL}'}}};")
+            out.append(f"{ind}    anvil_check({ptr}, {b.numel}LL, {mode}, {host}, {c_string(name)}, dims_, {len(b.shape)}, "
+                       f"{desc}, ins_, {len(inputs)});")
+            out.append(f"{ind}}}")
+        return out
+
+    @staticmethod
+    def describe(k: ir.Kernel) -> str:
+        """Where a kernel comes from (aarch64.py:82-89), when the program did not record it."""
+        head = f"  made by `{k.label or 'a computation'}`"
+        line = ""
+        span = k.span
+        if span is not None and span.location():
+            head += f" at {span.location()}"
+            if getattr(span, "src", None):
+                line = "\n      " + span.src
+        return f"{head}:{line}\n  computing ({k.name}):  {ir.fmt_kernel(k)}"
 
     def segment(self, seg: list, ind: str) -> list[str]:
         """A graph segment: a function that records the run (host kernels, twins, launches) and one
@@ -966,15 +1032,19 @@ class HipGen:
 # ----------------------------------------------------------------------------- plugin API
 
 def generate(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bool = False,
-             graphs: bool | None = None) -> str:
+             graphs: bool | None = None, check: str | None = None) -> str:
     """The .hip source of a program (library=True: a function lowered by pyapi.lower, called
     through anvil_entry with the input/output slots). emulate=True: a CPU build of the same
     program for testing the generator on a machine without a GPU. graphs=True: loop bodies are
     captured into HIP graphs and replayed (default: $ANVIL_HIP_GRAPHS, else off — on MI355X with
-    ROCm 7.2 eager launches measured faster for the C2 training step)."""
+    ROCm 7.2 eager launches measured faster for the C2 training step). check="nan" | "inf": the
+    reference's `--check` (cli.py:44-45): after each kernel, stop at the first nan (or infinity) it
+    wrote and say which computation made it."""
     if graphs is None:
         graphs = os.environ.get("ANVIL_HIP_GRAPHS", "0") == "1"
-    return HipGen(prog, seed=seed, library=library, emulate=emulate, graphs=graphs).generate()
+    if check not in (None, "nan", "inf"):
+        raise ValueError(f"check must be None, 'nan' or 'inf', not {check!r}")
+    return HipGen(prog, seed=seed, library=library, emulate=emulate, graphs=graphs, check=check).generate()
 
 
 def hipcc() -> str:

@@ -2,7 +2,7 @@
 
     python -m anvil hip   PROG.json [-o PROG.hip] [--seed N]     write the generated .hip file
     python -m anvil build PROG.json [-o PROG.so]  [--seed N]     compile it for gfx950
-    python -m anvil run   PROG.json [--seed N] [--profile] [--dump OUT.npz --keep a,b,...]
+    python -m anvil run   PROG.json [--seed N] [--profile] [--check[=inf]] [--dump OUT.npz --keep a,b,...]
     python -m anvil export FN.json [-o DIR] [--name LIB]        a function as lib<LIB>.so + <LIB>.h
 
 These mirror the reference's `anvil cuda file.anvil` and `anvil run|build --cuda` (cli.py:259-270,
@@ -43,6 +43,9 @@ def main(argv=None) -> int:
         q.add_argument("--emulate", action="store_true", help="a CPU build of the generated file (testing)")
         q.add_argument("--graphs", action="store_true", default=None,
                        help="replay loop bodies as HIP graphs (default: $ANVIL_HIP_GRAPHS)")
+        q.add_argument("--check", nargs="?", const="nan", choices=["nan", "inf"], default=None,
+                       help="stop at the first nan a computation makes, and say which line made it and how "
+                            "(--check=inf: at the first infinity too)")
         if name in ("hip", "build"):
             q.add_argument("-o", "--output", default=None)
         if name == "run":
@@ -64,7 +67,7 @@ def main(argv=None) -> int:
     from .backend import hip
     prog, data = _load_program(args.program)
     seed = args.seed if args.seed is not None else int(data.get("seed", 0))
-    src = hip.generate(prog, seed=seed, emulate=args.emulate, graphs=args.graphs)
+    src = hip.generate(prog, seed=seed, emulate=args.emulate, graphs=args.graphs, check=args.check)
     if args.cmd == "hip":
         out = args.output or os.path.splitext(args.program)[0] + ".hip"
         with open(out, "w") as f:

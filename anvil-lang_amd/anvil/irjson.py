@@ -104,8 +104,16 @@ class _Dumper:
                 stmts.append({"t": "store", "buf": self.buf(s.buf), "offset": self.aff(s.offset, lets),
                               "value": self.expr(s.value, lets), "acc": bool(s.accumulate)})
         line = getattr(k.span, "line", None) if k.span is not None else None
-        return {"id": k.id, "name": k.name, "label": k.label, "line": line,
-                "domain": [self.var(v) for v in k.domain], "red": red, "stmts": stmts}
+        out = {"id": k.id, "name": k.name, "label": k.label, "line": line,
+               "domain": [self.var(v) for v in k.domain], "red": red, "stmts": stmts}
+        loc = self.loc(k.span)
+        if loc:                                         # where the kernel comes from (--check messages)
+            out["loc"] = loc
+            try:
+                out["src"] = k.span.file.line_text(k.span.line).strip()
+            except Exception:
+                pass
+        return out
 
     @staticmethod
     def loc(span):
@@ -207,9 +215,10 @@ def _fnum(v):
 class _Span:
     """A source location that only knows its text (what error messages print) and line."""
 
-    def __init__(self, text, line=None):
+    def __init__(self, text, line=None, src=None):
         self.text = text
         self.line = line
+        self.src = src                  # the text of the source line, when the program recorded it
 
     def location(self):
         return self.text
@@ -308,8 +317,11 @@ def load(data) -> "ir.Program":
                 stmts.append(ir.Store(bufs[sd["buf"]], aff(sd["offset"], lets), expr(sd["value"], lets),
                                       bool(sd["acc"])))
         max_id = max(max_id, kd["id"])
-        span = None if kd.get("line") is None else _Span(None, kd["line"])
-        return ir.Kernel(domain, stmts, red, name=kd["name"], label=kd["label"], span=span, id=kd["id"])
+        span = None if kd.get("line") is None else _Span(kd.get("loc"), kd["line"], kd.get("src"))
+        k = ir.Kernel(domain, stmts, red, name=kd["name"], label=kd["label"], span=span, id=kd["id"])
+        if kd.get("desc"):
+            k.desc = kd["desc"]                         # what --check says about it, as recorded
+        return k
 
     def bound(x):
         return x if isinstance(x, int) else bufs[x["buf"]]

@@ -182,6 +182,22 @@ def _strides(shape):
     return out[::-1]
 
 
+def check_description(k) -> str:
+    """Where a kernel comes from, for --check (aarch64.py:82-89): the description the program
+    recorded for it, else its label, source location and line, and its computation."""
+    if getattr(k, "desc", None):
+        return k.desc
+    head = f"  made by `{k.label or 'a computation'}`"
+    line = ""
+    span = getattr(k, "span", None)
+    if span is not None and span.location():
+        head += f" at {span.location()}"
+        if getattr(span, "src", None):
+            line = "\n      " + span.src
+    from anvil import ir
+    return f"{head}:{line}\n  computing ({k.name}):  {ir.fmt_kernel(k)}"
+
+
 class Machine:
     """Runs an `ir.Program` (this package's IR, or anything with the same shape) on the CPU.
 
@@ -190,8 +206,10 @@ class Machine:
     StopRun to end the run (the CPU baseline times a bounded sample this way).
     """
 
-    def __init__(self, prog, out=None, seed: int = 0, inp=None, float_dtype=np.float32, loop_hook=None):
+    def __init__(self, prog, out=None, seed: int = 0, inp=None, float_dtype=np.float32, loop_hook=None,
+                 check=None):
         self.prog = prog
+        self.check = check                # "nan" | "inf": stop at the first nan (or infinity) a kernel makes
         self.out = out if out is not None else sys.stdout
         self.inp = inp if inp is not None else sys.stdin
         self.fdt = float_dtype
@@ -465,6 +483,24 @@ class Machine:
                 self.evaluate(k, dom, red, (v0, lo, min(v0.extent, lo + per)), stream)
         else:
             self.evaluate(k, dom, red, None, stream, chunk_reduction=True)
+        self.check_kernel(k)
+
+    def check_kernel(self, k):
+        """--check (interp.py:408-423): the first nan (or infinity) in a tensor k wrote ends the
+        program, with a message naming the tensor, the element and where the kernel comes from."""
+        if not self.check:
+            return
+        written = []
+        for st in k.stores:
+            if st.buf.root.dtype != "i32" and st.buf.root not in written:
+                written.append(st.buf.root)
+        for b in written:
+            a = self.arr(b)[:b.numel]
+            bad = np.isnan(a) if self.check == "nan" else ~np.isfinite(a)
+            if bad.any():
+                i = int(np.flatnonzero(bad)[0])
+                where = f" at {[int(v) for v in np.unravel_index(i, b.shape)]}" if b.shape else ""
+                raise RuntimeFault(f"--check: {a[i]} in `{b.name}`{where}\n{check_description(k)}")
 
     @staticmethod
     def grid(vars_, ranges):

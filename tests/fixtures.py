@@ -40,10 +40,16 @@ def run_oracle(prog, data, z=None, stdin=""):
     """Run the oracle on a fixture; function inputs come from the vectors file."""
     from oracle import interp
     out = io.StringIO()
-    m = interp.Machine(prog, out=out, seed=data.get("seed", 0), inp=io.StringIO(stdin))
+    m = interp.Machine(prog, out=out, seed=data.get("seed", 0), inp=io.StringIO(stdin), check=data.get("check"))
     if "function" in data and z is not None:
         by_id = {b.id: b for b in prog.buffers}
         for k, bid in enumerate(data["function"]["inputs"]):
             m.arr(by_id[bid])[:] = z[f"input{k}"].reshape(-1)
-    m.run()
+    m.check_error = ""
+    try:
+        m.run()
+    except interp.RuntimeFault as e:
+        if not data.get("check"):
+            raise
+        m.check_error = str(e)                          # --check stopped the program
     return m, out.getvalue()

@@ -55,7 +55,7 @@ def main(ref_root: str) -> None:
         name = spec["name"]
         if only and name not in only:
             continue
-        path = os.path.join(HERE, "programs", f"{name}.anvil")
+        path = spec.get("path") or os.path.join(HERE, "programs", f"{name}.anvil")
         if spec.get("function"):
             fn = spec["function"]
             sig = tuple(("tensor", tuple(shape), dtype) for shape, dtype in fn["args"])
@@ -66,9 +66,19 @@ def main(ref_root: str) -> None:
                                 "outputs": [None if b is None else b.id for b in low.outputs],
                                 "arg_names": list(low.arg_names), "out_names": list(low.out_names)}
         else:
-            prog = compile_text(spec["source"], path=path, consts=spec.get("consts")).program
+            prog = compile_text(spec["source"], path=path, consts=spec.get("consts"),
+                                optimize=spec.get("optimize", True)).program
             data = irjson.dump(prog)
+            if spec.get("check"):
+                # what --check says about each kernel (the reference's aarch64.check_description)
+                from anvil.backend.aarch64 import check_description
+                from anvil import ir as ref_ir
+                descs = {k.id: check_description(k) for k in ref_ir.all_kernels(prog)}
+                for kd in _kernels(data["main"]):
+                    kd["kernel"]["desc"] = descs[kd["kernel"]["id"]]
         data["seed"] = spec.get("seed", 0)
+        if spec.get("check"):
+            data["check"] = spec["check"]                # built and run with --check=<mode>
         with open(os.path.join(HERE, "ir", f"{name}.json"), "w") as f:
             json.dump(data, f, separators=(",", ":"))
         nk = sum(1 for _ in _kernels(data["main"]))
@@ -76,7 +86,8 @@ def main(ref_root: str) -> None:
         if not spec.get("interp"):
             continue
         out = io.StringIO()
-        it = Interpreter(prog, out=out, seed=spec.get("seed", 0), inp=io.StringIO(spec.get("stdin", "")))
+        it = Interpreter(prog, out=out, seed=spec.get("seed", 0), inp=io.StringIO(spec.get("stdin", "")),
+                         check=spec.get("check"))
         arrays = {}
         if spec.get("function"):
             rng = np.random.default_rng(spec["function"].get("input_seed", 2))
@@ -85,7 +96,15 @@ def main(ref_root: str) -> None:
                      else rng.integers(0, spec["function"].get("int_hi", 10), shape).astype(np.int32))
                 it.arr(b)[:b.numel] = x.reshape(-1)
                 arrays[f"input{k}"] = x
-        it.run()
+        arrays["check_error"] = np.frombuffer(b"", dtype=np.uint8)
+        try:
+            it.run()
+        except Exception as e:                           # --check: the interpreter's message
+            if not spec.get("check") or type(e).__name__ != "AnvilRuntimeError":
+                raise
+            arrays["check_error"] = np.frombuffer(str(e).encode(), dtype=np.uint8)
+        if not spec.get("check"):
+            del arrays["check_error"]
         by_name = {b.name: b for b in prog.buffers}
         for bname in spec.get("keep", []):
             b = by_name[bname]

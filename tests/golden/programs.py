@@ -176,6 +176,20 @@ print("loss {loss:.4f}")
 
 # ----------------------------------------------------------------------------- test programs
 
+CHECK_NAN = "x: [4, 3] ~ normal(0, 1)\nw = exp(x)\ny = log(x - 0.5) * w\nprint(sum(y))\n"
+
+CHECK_INF = "x: [4, 3] ~ normal(0, 1)\nz = log(x * 0)\nr = z - z\nprint(sum(r))\n"
+
+CHECK_HEALTHY = """
+x: [64, 8] ~ normal(0, 1)
+y: [64] ~ normal(0, 1)
+param w: [8] ~ normal(0, 1)
+for step in range(20):
+    loss = mean((x @ w - y) ** 2)
+    minimize loss with adam(lr=0.01)
+print(loss)
+"""
+
 HELLO = """
 x = [1.0, 2.0, 3.0]
 W = [[1.0, 0.0, -1.0],
@@ -439,6 +453,15 @@ PROGRAMS = [
      "function": {"name": "attention", "args": [([2, 128, 64], "f32")] * 3}},
     {"name": "c3_attention_d128", "source": C3_ATTENTION, "interp": True,
      "function": {"name": "attention", "args": [([2, 256, 128], "f32")] * 3}},
+    # --check (the reference's tests/test_native.py:292-320): unoptimized, one kernel per operation
+    {"name": "check_nan", "source": CHECK_NAN, "interp": True, "optimize": False, "check": "nan",
+     "path": "checked.anvil"},
+    {"name": "check_inf", "source": CHECK_INF, "interp": True, "optimize": False, "check": "nan",
+     "path": "checked.anvil"},
+    {"name": "check_inf_traced", "source": CHECK_INF, "interp": True, "optimize": False, "check": "inf",
+     "path": "checked.anvil"},
+    {"name": "check_healthy", "source": CHECK_HEALTHY, "interp": True, "optimize": False, "check": "inf",
+     "path": "checked.anvil"},
     # the reference's CUDA backend test cases as programs
     {"name": "hello", "source": HELLO, "interp": True},
     {"name": "linreg", "source": LINREG, "interp": True, "keep": ["w", "b"]},

@@ -26,7 +26,8 @@ from fixtures import ROOT_PKG, ir_path, load_ir, vectors
 NUMBER = re.compile(r"[-+]?(?:\d+\.\d*|\.\d+|\d+)(?:[eE][-+]?\d+)?|[-+]?inf|nan")
 
 
-def run_program(name_or_path: str, emulate: bool, keep=(), timeout: int = 600, cwd=None, env_extra=None):
+def run_program(name_or_path: str, emulate: bool, keep=(), timeout: int = 600, cwd=None, env_extra=None,
+                check=None):
     """(exit status, stdout, stderr, {buffer name: final contents})."""
     path = name_or_path if name_or_path.endswith(".json") else ir_path(name_or_path)
     with tempfile.TemporaryDirectory() as d:
@@ -34,6 +35,8 @@ def run_program(name_or_path: str, emulate: bool, keep=(), timeout: int = 600, c
         cmd = [sys.executable, "-u", "-m", "anvil", "run", path]
         if emulate:
             cmd.append("--emulate")
+        if check:
+            cmd.append(f"--check={check}")
         if keep:
             cmd += ["--dump", dump, "--keep", ",".join(keep)]
         env = dict(os.environ, PYTHONPATH=ROOT_PKG + os.pathsep + os.environ.get("PYTHONPATH", ""))

@@ -21,6 +21,9 @@ def test_oracle_matches_reference_interpreter(name):
     z = vectors(name)
     m, out = run_oracle(prog, data, z)
     assert out == stdout_of(z)
+    if "check_error" in z.files:                       # --check: the same element, tensor and message
+        assert m.check_error == bytes(z["check_error"]).decode()
+        return
     by_name = {b.name: b for b in prog.buffers}
     by_id = {b.id: b for b in prog.buffers}
     for key in z.files:
