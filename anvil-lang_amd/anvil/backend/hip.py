@@ -327,7 +327,8 @@ class HipGen:
         The scan may cross one `if (host scalar) break;` (a step limit checked after the batch is
         gathered): the launch then goes after the check, and the leaving path launches the parts
         that came before the check on their own, so they run exactly when they did."""
-        if self.emulate or self.check or os.environ.get("ANVIL_HIP_SIDE", "1") == "0":
+        if (self.emulate or self.check or os.environ.get("ANVIL_HIP_SIDE", "1") == "0"
+                or getattr(plan, "kslices", 1) > 1):
             return plan, used
         ids = lambda bs: {b.root.id for b in bs}
 
@@ -361,7 +362,7 @@ class HipGen:
                 j += 1
                 continue
             cand, cused = self.plan_run(stmts, j)
-            if cand.kind in ("serial", "fused"):
+            if cand.kind in ("serial", "fused") or getattr(cand, "kslices", 1) > 1:
                 break
             moved = between + list(getattr(cand, "hoisted", []))
             if {st2.buf.root.id for h in moved for st2 in h.stores} & reads:
@@ -546,6 +547,11 @@ class HipGen:
                         if twin is not None:
                             seg.append(("twin", self.launch(twin, ind), twin))
                 seg.append(("launch", self.launch(plan, ind), plan))
+                if getattr(plan, "kslices", 1) > 1:           # a K split across workgroups: its sum
+                    if not hasattr(plan, "reduce_plan"):
+                        plan.reduce_plan = self.gemm.GemmReducePlan(plan)
+                        self.plans.append(plan.reduce_plan)
+                    seg.append(("launch", self.launch(plan.reduce_plan, ind), plan.reduce_plan))
                 if self.check:
                     for kk in plan.kernels:
                         seg.append(("host", self.check_lines(kk, ind), None))

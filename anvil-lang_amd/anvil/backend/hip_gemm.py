@@ -26,6 +26,7 @@ from .hip_kernels import KernelScope, Plan, canon_key, decode
 MIN_WORK = 1 << 16           # M·N·K below which the generic schedules are as good
 MIN_SIDE = 32                # a narrower product (10 classes) wastes most of a 32-wide MFMA tile
 CUS = 256                    # compute units of an MI355X
+CU_WAVES = CUS * 4           # wavefronts that fill it once (one per SIMD)
 
 
 def _factors(e, out):
@@ -143,8 +144,18 @@ def analyse(k: ir.Kernel):
         if any(not ca(v) and not cb(v) for v in bv) or not mv or not nv:
             continue
         km = _merge(rv, ca, cb)
+        kmulti = None
         if km is None:
-            continue
+            # K over several variables that are not one linear index of both operands (a weight
+            # gradient summed over the batch and a convolution's positions): k decomposes over
+            # them, outer to inner; the innermost is the most contiguous and a multiple of 8 (a
+            # pipelined chunk of 8 k never straddles two of its runs)
+            inner = min(rv, key=lambda v: (min(abs(ca(v)), abs(cb(v))), v.id))
+            order = sorted([v for v in rv if v is not inner], key=lambda v: (-abs(ca(v)), v.id)) + [inner]
+            if inner.extent % 8:
+                continue
+            km = (order, ca(inner))
+            kmulti = [(v.extent, ca(v), cb(v)) for v in order]
         mm = _merge(mv, ca)
         if mm is None:                                   # keep the densest one as m, batch the rest
             inner = min(mv, key=lambda v: (abs(ca(v)), v.id))
@@ -168,6 +179,7 @@ def analyse(k: ir.Kernel):
         s.K = ir.prod(v.extent for v in s.k_vars)
         s.B = ir.prod(v.extent for v in s.batch)
         s.a_gather, s.b_gather = gathered_row(la), gathered_row(lb)
+        s.k_multi = kmulti
         if (s.a_gather and (s.m_vars != [s.a_gather[2]] or s.batch or any(ca(v) for v in nv))) or \
                 (s.b_gather and (s.n_vars != [s.b_gather[2]] or s.batch or any(cb(v) for v in mv))):
             continue                                    # rows picked through an index: one plain row variable
@@ -188,11 +200,14 @@ def load_mode(rs, ks, T, K, const, batch_strides):
 
 
 def gathered_ok(s) -> bool:
-    """Operands with gathered rows are supported by the pipelined K split only, loading 16 bytes
-    along k from each row (so K a multiple of 8, rows starting on 16 bytes)."""
+    """Operands with gathered rows, and K over several variables, are supported by the pipelined K
+    split only; gathered rows load 16 bytes along k (so K a multiple of 8, rows on 16 bytes)."""
+    pipe = os.environ.get("ANVIL_GEMM_PIPE", "1") != "0"
     for g, rs, ks, T in ((s.a_gather, s.a_rs, s.a_ks, s.M), (s.b_gather, s.b_rs, s.b_ks, s.N)):
-        if g is not None and (s.K % 8 or ks != 1 or g[1] % 4 or os.environ.get("ANVIL_GEMM_PIPE", "1") == "0"):
+        if g is not None and (s.K % 8 or ks != 1 or g[1] % 4 or not pipe):
             return False
+    if s.k_multi and (not pipe or s.batch):
+        return False
     return True
 
 
@@ -435,10 +450,21 @@ class GemmPlan(Plan):
             else:
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.waves, self.unroll = int(parts[1]), int(parts[2])
-        if s.a_gather or s.b_gather:                    # gathered rows: the pipelined K split only
+        if s.a_gather or s.b_gather or s.k_multi:       # the pipelined K split only
             self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
         self.pipe = self.pipe and self.sched == "ksplit" and not self.slab
-        nch = -(-(s.K // 8) // self.waves)                  # chunks per wave
+        # K split across workgroups as well, when the output has few tiles and K is long (a
+        # convolution's weight gradient: 64 x 288 outputs, K = 73728): each workgroup computes a
+        # slice of K into a partial tile, and a second kernel adds the S partials in order and runs
+        # the epilogue (see GemmReducePlan)
+        tiles = -(-s.M // 32) * -(-s.N // 32) * s.B
+        self.kslices, self.kslice = 1, s.K
+        if (self.pipe and tiles * self.waves < CU_WAVES // 2 and s.K >= 4096
+                and os.environ.get("ANVIL_GEMM_SPLITK", "1") != "0"):
+            S = max(2, min(1024 // tiles, s.K // 512))
+            self.kslice = -(-(-(-s.K // S)) // 8) * 8
+            self.kslices = -(-s.K // self.kslice)
+        nch = -(-(self.kslice // 8) // self.waves)          # chunks per wave
         self.depth = max(1, min(int(os.environ.get("ANVIL_GEMM_DEPTH", "2" if nch <= 32 else "4")), nch))
         self.threads = 64 * self.waves if self.sched == "ksplit" else 256
         self.tm = -(-s.M // self.BM)
@@ -483,7 +509,7 @@ class GemmPlan(Plan):
         self.label += " + " + (e.label or e.name)
 
     def grid(self):
-        return (self.tn, self.tm, self.s.B), self.threads
+        return (self.tn, self.tm, self.s.B * self.kslices), self.threads
 
     def row_fn(self, sc, name, gather, rs) -> str:
         """A device lambda: where row t of an operand starts (t·rs, or c·idx[t + ...] for a gathered
@@ -513,6 +539,78 @@ class GemmPlan(Plan):
         sc.fwd, sc.canon = saved
         return "\n".join([f"    auto {name} = [=](float x) -> float {{"] + lines + [f"        return {v};", "    };"])
 
+    def k_fn(self, name, which) -> str:
+        """A device lambda: where k-index k of an operand starts (k·stride, or the offsets of the
+        several K variables it decomposes into)."""
+        s = self.s
+        if not s.k_multi:
+            ks = s.a_ks if which == "a" else s.b_ks
+            return f"    auto {name} = [=](int k) -> long long {{ return (long long)k * {ks}LL; }};"
+        parts, rest = [], "k"
+        for depth, (ext, sa, sb) in enumerate(reversed(s.k_multi)):
+            st = sa if which == "a" else sb
+            outer = depth == len(s.k_multi) - 1
+            idx = rest if outer else f"({rest} % {ext})"
+            if st:
+                parts.append(f"{st}LL * (long long){idx}")
+            rest = f"({rest} / {ext})"
+        return f"    auto {name} = [=](int k) -> long long {{ return {' + '.join(parts) or '0LL'}; }};"
+
+    def ws_buffer(self):
+        """The partial tiles of a K split across workgroups: [slice][batch][M][N] floats."""
+        if not hasattr(self, "_ws"):
+            s = self.s
+            self._ws = ir.Buffer(f"{self.name}.partials", (self.kslices * s.B * s.M * s.N,), F32, "scratch",
+                                 id=800_000_000 + self.k.id)
+        return self._ws
+
+    def epilogue(self, sc, loop, slot, value, hoisted, per):
+        """The statements of the product's kernel and its followers for each of the lane's output
+        elements (the loop), with acc = alpha · value; hoisted: loads issued before the K loop."""
+        s, k = self.s, self.k
+        stages = [(k, None, [])] + list(self.followers)
+
+        def element_vars(em):
+            for line in decode(s.m_vars, "(uint32_t)mi", "uint32_t"):
+                em.emit(line)
+            for line in decode(s.n_vars, "(uint32_t)ni", "uint32_t"):
+                em.emit(line)
+            for e, m, _ in self.followers:
+                for ev, aff in m.items():
+                    em.emit(f"const int v{ev.id} = (int)({em.affine(aff)});")
+        pre = []
+        if hoisted:
+            pre.append("    " + " ".join(f"float pre{i}[{per}];" for i in range(len(hoisted))))
+            pre += loop
+            pl: list[str] = []
+            pem = Emitter(sc, pl, "        ", prefix="p")
+            element_vars(pem)
+            for i, (si, ld) in enumerate(hoisted):
+                pem.emit(f"pre{i}[{slot}] = {pem.build(ld)};")
+            pre += pl + ["    }"]
+        body = loop + [f"        const float acc_v = {flit(s.alpha)} * {value};"]
+        lines: list[str] = []
+        em = Emitter(sc, lines, "        ")
+        element_vars(em)
+        strides = ir.row_major_strides([v.extent for v in k.domain])
+        sc.rand = " + ".join(f"{st}u * (uint32_t)v{v.id}" for v, st in zip(k.domain, strides)) or "0u"
+        sc.acc_name = "acc_v"
+        stored = {}
+
+        def on_store(st, val):
+            stored[st.buf.root.id] = val
+        for si, (e, m, fwd) in enumerate(stages):
+            em.reset_memo()
+            canon = {v: ("e", v.id) for v in e.domain}
+            sc.canon = canon
+            sc.fwd = {canon_key(ld.buf, ld.offset, canon): stored[ld.buf.root.id] for ld in fwd}
+            for i, (sj, ld) in enumerate(hoisted):
+                if sj == si:
+                    sc.fwd[canon_key(ld.buf, ld.offset, canon)] = f"pre{i}[{slot}]"
+            self.statements(em, e, sc, parallel=True, on_store=on_store)
+        sc.canon, sc.fwd = None, {}
+        return pre, body + lines + ["    }"]
+
     def source(self) -> str:
         s, k = self.s, self.k
         sc = KernelScope(self)
@@ -525,8 +623,12 @@ class GemmPlan(Plan):
         ca, cb = s.la.offset.coef, s.lb.offset.coef
         a_off = [str(s.la.offset.const)]
         b_off = [str(s.lb.offset.const)]
+        zsrc = "blockIdx.z"
+        if self.kslices > 1:
+            body.append(f"    const uint32_t slice = blockIdx.z % {self.kslices}u, bz = blockIdx.z / {self.kslices}u;")
+            zsrc = "bz"
         if s.batch:
-            body += ["    " + line for line in decode(s.batch, "blockIdx.z", "uint32_t")]
+            body += ["    " + line for line in decode(s.batch, zsrc, "uint32_t")]
             for v in s.batch:
                 if ca(v):
                     a_off.append(f"{ca(v)}LL * v{v.id}")
@@ -558,19 +660,25 @@ class GemmPlan(Plan):
                     "        const int ni = n0 + (lane & 31);",
                     f"        if (mi >= {s.M} || ni >= {s.N}) continue;"]
             slot = "q"
+            chk = lambda n: "true" if n % 32 else "false"
             if self.slab:
                 kargs = (f"pa, {s.a_rs}LL, {s.a_ks}LL, pb, {s.b_rs}LL, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, {s.K}, "
                          "opa, opb")
-                chk = lambda n: "true" if n % 32 else "false"
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_kslab<{self.amode}, {self.bmode}, {self.slab}, {chk(s.M)}, {chk(s.N)}>"
                         f"(part, {kargs});"]
             elif self.pipe:
-                body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs), self.row_fn(sc, "brow", s.b_gather, s.b_rs)]
-                kargs = (f"pa, arow, {s.a_ks}LL, pb, brow, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, {s.K}, "
+                body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs), self.row_fn(sc, "brow", s.b_gather, s.b_rs),
+                         self.k_fn("ak", "a"), self.k_fn("bk", "b")]
+                if self.kslices > 1:
+                    krange = (f"(int)slice * {self.kslice}, min({self.kslice}, {s.K} - (int)slice * {self.kslice})")
+                else:
+                    krange = f"0, {s.K}"
+                a_ks = s.a_ks if not s.k_multi else s.k_multi[-1][1]
+                b_ks = s.b_ks if not s.k_multi else s.k_multi[-1][2]
+                kargs = (f"pa, arow, ak, {a_ks}LL, pb, brow, bk, {b_ks}LL, {s.M}, {s.N}, m0, n0, {krange}, "
                          "opa, opb")
-                chk = lambda n: "true" if n % 32 else "false"
-                nch = -(-(s.K // 8) // W)
+                nch = -(-(self.kslice // 8) // W)
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_kpipe<{W}, 1, 1, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
                         f"{chk(s.M)}, {chk(s.N)}>(part, {kargs});"]
@@ -578,56 +686,62 @@ class GemmPlan(Plan):
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]
             value = "part[0][0][q]"
-        stages = [(k, None, [])] + list(self.followers)
-        hoisted = self.hoistable(stages) if per * 4 <= 64 and os.environ.get("ANVIL_GEMM_HOIST", "1") != "0" else []
-        hoisted = hoisted[:max(0, 64 // per)]
+        def head():                                   # after the body: its buffers are the parameters
+            return [self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
+                    + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, B {self.bmode[9:]}"
+                    + (f" · K in {self.kslices} slices of {self.kslice}, partial tiles" if self.kslices > 1 else "")
+                    + (f" · K over {len(s.k_multi)} variables" if s.k_multi else ""),
+                    self.header(self.threads)]
+        if self.kslices > 1:
+            # partial tiles only: GemmReducePlan adds them up and runs the epilogue
+            ws = sc.buf(self.ws_buffer())
+            store = loop + [f"        {ws}[(((long long)slice * {s.B} + bz) * {s.M} + mi) * {s.N} + ni] = {value};",
+                            "    }"]
+            return "\n".join(head() + body + main + store + ["}"])
+        hoisted = []
+        if per * 4 <= 64 and os.environ.get("ANVIL_GEMM_HOIST", "1") != "0":
+            hoisted = self.hoistable([(k, None, [])] + list(self.followers))[:max(0, 64 // per)]
+        pre, post = self.epilogue(sc, loop, slot, value, hoisted, per)
+        return "\n".join(head() + body + pre + main + post + ["}"])
 
-        def element_vars(em):
-            for line in decode(s.m_vars, "(uint32_t)mi", "uint32_t"):
-                em.emit(line)
-            for line in decode(s.n_vars, "(uint32_t)ni", "uint32_t"):
-                em.emit(line)
-            for e, m, _ in self.followers:
-                for ev, aff in m.items():
-                    em.emit(f"const int v{ev.id} = (int)({em.affine(aff)});")
-        # epilogue operands that do not depend on the product are loaded before the K loop
-        if hoisted:
-            body.append("    " + " ".join(f"float pre{i}[{per}];" for i in range(len(hoisted))))
-            body += loop
-            pl: list[str] = []
-            pem = Emitter(sc, pl, "        ", prefix="p")
-            element_vars(pem)
-            for i, (si, ld) in enumerate(hoisted):
-                pem.emit(f"pre{i}[{slot}] = {pem.build(ld)};")
-            body += pl + ["    }"]
-        body += main
-        body += loop + [f"        const float acc_v = {flit(s.alpha)} * {value};"]
-        lines: list[str] = []
-        em = Emitter(sc, lines, "        ")
-        element_vars(em)
-        strides = ir.row_major_strides([v.extent for v in k.domain])
-        sc.rand = " + ".join(f"{st}u * (uint32_t)v{v.id}" for v, st in zip(k.domain, strides)) or "0u"
-        sc.acc_name = "acc_v"
-        stored = {}
 
-        def on_store(st, val):
-            stored[st.buf.root.id] = val
-        for si, (e, m, fwd) in enumerate(stages):
-            em.reset_memo()
-            canon = {v: ("e", v.id) for v in e.domain}
-            sc.canon = canon
-            sc.fwd = {canon_key(ld.buf, ld.offset, canon): stored[ld.buf.root.id] for ld in fwd}
-            for i, (sj, ld) in enumerate(hoisted):
-                if sj == si:
-                    sc.fwd[canon_key(ld.buf, ld.offset, canon)] = f"pre{i}[{slot}]"
-            self.statements(em, e, sc, parallel=True, on_store=on_store)
-        sc.canon, sc.fwd = None, {}
-        body += lines
-        body += ["    }", "}"]
-        head = [self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
-                + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, B {self.bmode[9:]}",
-                self.header(self.threads)]
-        return "\n".join(head + body)
+class GemmReducePlan(Plan):
+    """The second kernel of a K split across workgroups: for each output element, the S partial
+    tiles added in slice order (the result does not depend on timing), then the product kernel's
+    statements and its followers' (a weight update)."""
+
+    kind = "gemm-reduce"
+
+    def __init__(self, gemm: "GemmPlan"):
+        super().__init__(gemm.gen, [], gemm.name + "r")
+        self.gemm = gemm
+        self.label = "partial-tile sum + " + gemm.label
+        s = gemm.s
+        self.total = s.B * s.M * s.N
+        self.blocks = max(1, min(-(-self.total // 256), 1 << 16))
+        self.streams = list(gemm.streams)
+
+    def grid(self):
+        return self.blocks, 256
+
+    def source(self) -> str:
+        g, s = self.gemm, self.gemm.s
+        self.skip_stores = g.skip_stores
+        sc = KernelScope(self)
+        sc.stream_name = g.stream_param(g.k)
+        ws = sc.buf(g.ws_buffer())
+        body = [f"    for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < {self.total}u; e += gridDim.x * 256u) {{",
+                f"        const uint32_t bz = e / {s.M * s.N}u;",
+                f"        const int mi = (int)((e / {s.N}u) % {s.M}u), ni = (int)(e % {s.N}u);"]
+        body += ["        " + line for line in decode(s.batch, "bz", "uint32_t")]
+        body += ["        float sum = 0.0f;",
+                 f"        for (int sl = 0; sl < {g.kslices}; sl++) "
+                 f"sum += {ws}[(((long long)sl * {s.B} + bz) * {s.M} + mi) * {s.N} + ni];"]
+        # the epilogue's statements, for this one element (its buffers become this kernel's)
+        _, post = g.epilogue(sc, [], "0", "sum", [], 1)
+        head = [f"// gemm-reduce: {g.name}: {g.kslices} partial tiles of {s.M}x{s.N}" + (f" x{s.B}" if s.B > 1 else "")
+                + " added in order, then the epilogue", self.header(256)]
+        return "\n".join(head + body + post[:-1] + ["    }", "}"])
 
 
 def _key(ld):

@@ -270,40 +270,46 @@ __device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][16 / W
 // straight-line code, where the compiler's wait counts are exact. Rows and columns past M / N are
 // zero (CHKM, CHKN: the tile may cross the edge); k is always in range. Where row (column) t of
 // an operand starts is arow(t) (brow(t)): t times its stride, or, for rows picked through an index
-// array (a shuffled batch, X[perm[i]]), that row's offset; each lane computes its rows' once.
+// array (a shuffled batch, X[perm[i]]), that row's offset; each lane computes its rows' once. Where
+// k-index k starts is ak(k) (bk(k)): k times the stride, or, when K runs over several loop
+// variables (a weight gradient summed over the batch and the positions of a convolution), their
+// offsets; 4 consecutive k are a_ks (b_ks) apart. The workgroup covers k in [kbeg, kbeg + K).
 template <int MODE, bool CHK>
-__device__ __forceinline__ void anvil_chunk_load_k(float (&r)[4], const float *__restrict__ p, long long toff, long long ks,
-                                                   int t, int tmax, int k) {
+__device__ __forceinline__ void anvil_chunk_load_k(float (&r)[4], const float *__restrict__ p, long long toff,
+                                                   long long koff, long long ks, int t, int tmax) {
     if (CHK && t >= tmax) {
         r[0] = r[1] = r[2] = r[3] = 0.f;
         return;
     }
     if (MODE == ANVIL_LD_KC) {
-        const anvil_f32x4 v = *(const anvil_f32x4 *)(p + toff + k);
+        const anvil_f32x4 v = *(const anvil_f32x4 *)(p + toff + koff);
         r[0] = v.x;
         r[1] = v.y;
         r[2] = v.z;
         r[3] = v.w;
     } else {
 #pragma unroll
-        for (int s = 0; s < 4; s++) r[s] = p[toff + (long long)(k + s) * ks];
+        for (int s = 0; s < 4; s++) r[s] = p[toff + koff + (long long)s * ks];
     }
 }
 
-template <int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, bool FULL, class OPA, class OPB>
+template <int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, bool FULL, class AK, class BK,
+          class OPA, class OPB>
 __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
-                                                    const float *__restrict__ a, const long long (&ao)[TM], long long a_ks,
-                                                    const float *__restrict__ b, const long long (&bo)[TN], long long b_ks,
+                                                    const float *__restrict__ a, const long long (&ao)[TM], AK ak,
+                                                    long long a_ks, const float *__restrict__ b,
+                                                    const long long (&bo)[TN], BK bk, long long b_ks,
                                                     int M, int N, int m0, int n0, int c0, int n, OPA opa, OPB opb) {
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     float ab[D][TM][4], bb[D][TN][4];
 #define ANVIL_KP_LOAD(d, c)                                                                                \
     if (FULL || (c) < n) {                                                                                 \
         const int k_ = 8 * (c0 + (c)) + 4 * h;                                                             \
+        const long long ka_ = ak(k_), kb_ = bk(k_);                                                        \
         _Pragma("unroll") for (int i = 0; i < TM; i++)                                                     \
-            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, ao[i], a_ks, m0 + 32 * i + r, M, k_);            \
+            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, ao[i], ka_, a_ks, m0 + 32 * i + r, M);           \
         _Pragma("unroll") for (int j = 0; j < TN; j++)                                                     \
-            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, bo[j], b_ks, n0 + 32 * j + r, N, k_);            \
+            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, bo[j], kb_, b_ks, n0 + 32 * j + r, N);           \
     }
 #pragma unroll
     for (int c = 0; c < D; c++) ANVIL_KP_LOAD(c, c)
@@ -327,16 +333,16 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
 }
 
 template <int W, int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, class AROW, class BROW,
-          class OPA, class OPB>
+          class AK, class BK, class OPA, class OPB>
 __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W],
-                                                    const float *__restrict__ a, AROW arow, long long a_ks,
-                                                    const float *__restrict__ b, BROW brow, long long b_ks,
-                                                    int M, int N, int m0, int n0, int K, OPA opa, OPB opb) {
+                                                    const float *__restrict__ a, AROW arow, AK ak, long long a_ks,
+                                                    const float *__restrict__ b, BROW brow, BK bk, long long b_ks,
+                                                    int M, int N, int m0, int n0, int kbeg, int K, OPA opa, OPB opb) {
     constexpr int PER = 16 / W;
     __shared__ float part[W * TM * TN * 16 * 64];
     const int lane = threadIdx.x & 63, r = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     // uniform: scalar branches
-    const int c0 = w * NCH, n = min(NCH, max(0, (K >> 3) - c0));
+    const int c0 = (kbeg >> 3) + w * NCH, n = min(NCH, max(0, ((kbeg + K) >> 3) - c0));
     long long ao[TM], bo[TN];
 #pragma unroll
     for (int i = 0; i < TM; i++) ao[i] = (!CHKM || m0 + 32 * i + r < M) ? arow(m0 + 32 * i + r) : 0;
@@ -345,11 +351,11 @@ __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W]
     anvil_mm_acc<TM, TN> acc;
     acc.zero();
     if (n == NCH)
-        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, true>(acc, a, ao, a_ks, b, bo, b_ks, M, N,
+        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, true>(acc, a, ao, ak, a_ks, b, bo, bk, b_ks, M, N,
                                                                             m0, n0, c0, n, opa, opb);
     else if (n > 0)
-        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, false>(acc, a, ao, a_ks, b, bo, b_ks, M, N,
-                                                                             m0, n0, c0, n, opa, opb);
+        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, false>(acc, a, ao, ak, a_ks, b, bo, bk, b_ks, M,
+                                                                             N, m0, n0, c0, n, opa, opb);
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll

@@ -440,6 +440,10 @@ PROGRAMS = [
      "consts": {"STEPS": 3, "BATCH": 2, "T": 8, "D": 32, "HEADS": 2, "LAYERS": 2}, "interp": True},
     {"name": "c5_small", "source": C5, "consts": {"STEPS": 3, "NB": 4, "C1": 4, "C2": 8, "HID": 16},
      "interp": True},
+    # C5 at a size where the convolution's weight gradient is a product with K over the batch and
+    # the positions, split across workgroups, and fc1 (32 x 32, K = 9216) splits K as well
+    {"name": "c5_mid", "source": C5, "consts": {"STEPS": 2, "NB": 32, "C1": 8, "C2": 32, "HID": 32},
+     "interp": True, "keep": ["net.c1.W", "net.c2.W", "net.fc1.W", "net.fc2.W"]},
     {"name": "c3_softmax_small", "source": C3_SOFTMAX, "interp": True,
      "function": {"name": "rows_softmax", "args": [([64, 300], "f32")]}},
     {"name": "c3_layernorm_small", "source": C3_LAYERNORM, "interp": True,
