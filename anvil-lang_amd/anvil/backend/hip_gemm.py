@@ -212,7 +212,10 @@ def gathered_ok(s) -> bool:
 
 
 def match(gen, k: ir.Kernel, name: str):
-    if gen.emulate or any(st.accumulate for st in k.stores):
+    """A GemmPlan for a contraction kernel (its stores may add to their buffer, `+=`: a gradient
+    that collects several products; the epilogue then adds atomically, as the reference's parallel
+    kernels do)."""
+    if gen.emulate:
         return None
     s = analyse(k)
     if s is None or s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < MIN_SIDE or not gathered_ok(s):
@@ -387,9 +390,12 @@ def follower(k: ir.Kernel, e: ir.Kernel, hosts: set):
         if st.buf.root.id in stored:
             return None
         stored[st.buf.root.id] = st.offset
+    added = {st.buf.root.id for st in k.stores if st.accumulate}   # k adds to them: no value to forward
     fwd = []
     for ld in A.kernel_loads(e):
         bid = ld.buf.root.id
+        if bid in added:
+            return None
         if bid in stored:
             sub = subst_affine(ld.offset, m)
             if sub is None or sub != stored[bid]:
@@ -598,7 +604,8 @@ class GemmPlan(Plan):
         stored = {}
 
         def on_store(st, val):
-            stored[st.buf.root.id] = val
+            if not st.accumulate:                     # an addition leaves no value to forward
+                stored[st.buf.root.id] = val
         for si, (e, m, fwd) in enumerate(stages):
             em.reset_memo()
             canon = {v: ("e", v.id) for v in e.domain}

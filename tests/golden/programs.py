@@ -438,6 +438,11 @@ PROGRAMS = [
      "interp": True, "keep": C2_KEEP},
     {"name": "c4_small", "source": C4,
      "consts": {"STEPS": 3, "BATCH": 2, "T": 8, "D": 32, "HEADS": 2, "LAYERS": 2}, "interp": True},
+    # C4 at a size where its products are matrix-core products, the input gradients that add
+    # q, k and v's contributions (`+=`) among them
+    {"name": "c4_mid", "source": C4,
+     "consts": {"STEPS": 2, "BATCH": 4, "T": 32, "D": 64, "HEADS": 2, "LAYERS": 1}, "interp": True,
+     "keep": ["net.E", "net.blocks.0.Wq", "net.blocks.0.up.W", "net.out.W"]},
     {"name": "c5_small", "source": C5, "consts": {"STEPS": 3, "NB": 4, "C1": 4, "C2": 8, "HID": 16},
      "interp": True},
     # C5 at a size where the convolution's weight gradient is a product with K over the batch and

@@ -15,10 +15,10 @@ from fixtures import load_ir, stdout_of, vectors
 from hiprun import function_call, kept_buffers, outputs_match, patched_program, run_program, tensors_match
 
 PROGRAMS = ["hello", "linreg", "attention_train", "split", "scatter", "integers", "formats", "control",
-            "products", "c1_small", "c2_small", "c2_steps100", "mnist_like", "c4_small", "c5_small", "c5_mid"]
+            "products", "c1_small", "c2_small", "c2_steps100", "mnist_like", "c4_small", "c4_mid", "c5_small", "c5_mid"]
 FUNCTIONS = ["c3_softmax_small", "c3_layernorm_small", "c3_linear_small", "c3_attention_small",
              "c3_attention_d64", "c3_attention_d128"]
-TRAINED = {"c2_steps100", "c2_small", "c1_small", "mnist_like", "linreg", "attention_train", "c5_mid"}
+TRAINED = {"c2_steps100", "c2_small", "c1_small", "mnist_like", "linreg", "attention_train", "c5_mid", "c4_mid"}
 
 
 @pytest.mark.parametrize("name", PROGRAMS)
