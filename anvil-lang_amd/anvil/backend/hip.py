@@ -116,6 +116,9 @@ class HipGen:
         if not emulate and not check and os.environ.get("ANVIL_HIP_GATHER_FWD", "1") != "0":
             from . import hip_gemm
             prog = hip_gemm.forward_gather_copies(prog, A.host_scalars(prog))
+        if not check and os.environ.get("ANVIL_HIP_IMPLICIT_CONV", "1") != "0":
+            from . import hip_conv
+            prog = hip_conv.forward_im2col_copies(prog)
         self.prog = prog
         self.seed = seed & 0xFFFFFFFF
         self.library = library
@@ -291,6 +294,9 @@ class HipGen:
         if not parallel:
             return HK.SerialPlan(self, k, name), 1
         if k.red is None:
+            scat = HK.scatter_targets(k)
+            if scat is not None:
+                return HK.GatherSumPlan(self, k, name, *scat), 1
             return HK.MapPlan(self, k, name), 1
         if self.gemm is not None:
             g = self.gemm.match(self, k, name)

@@ -169,6 +169,15 @@ def injective_over(off: ir.Affine, vars_) -> bool:
     return True
 
 
+def sole_writer(k: ir.Kernel, st) -> bool:
+    """Does each element of k's domain own the element that store `st` adds to? Its offset is
+    injective over the domain and has no gathers, and every other store of k to that buffer uses
+    the same offset. Then `+=` needs no atomic: no other lane of the launch touches the element."""
+    if st.offset.gathers() or not injective_over(st.offset, k.domain):
+        return False
+    return all(o.offset == st.offset for o in k.stores if o.buf.root is st.buf.root)
+
+
 def parallel_safe(k: ir.Kernel) -> bool:
     written = {}
     for st in k.stores:

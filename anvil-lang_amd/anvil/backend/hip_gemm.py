@@ -15,6 +15,7 @@ split off into a second kernel.
 """
 from __future__ import annotations
 
+import math
 import os
 
 from .. import ir
@@ -147,25 +148,38 @@ def analyse(k: ir.Kernel):
         kmulti = None
         if km is None:
             # K over several variables that are not one linear index of both operands (a weight
-            # gradient summed over the batch and a convolution's positions): k decomposes over
-            # them, outer to inner; the innermost is the most contiguous and a multiple of 8 (a
-            # pipelined chunk of 8 k never straddles two of its runs)
-            inner = min(rv, key=lambda v: (min(abs(ca(v)), abs(cb(v))), v.id))
-            order = sorted([v for v in rv if v is not inner], key=lambda v: (-abs(ca(v)), v.id)) + [inner]
-            if inner.extent % 8:
+            # gradient summed over the batch and a convolution's positions, or a convolution's
+            # channels and window): k decomposes over them, outer to inner; the innermost is the
+            # most contiguous of those whose extent is a multiple of 8 (a pipelined chunk of 8 k
+            # never straddles two of its runs)
+            fit = [v for v in rv if v.extent % 8 == 0]
+            if not fit:
                 continue
+            inner = min(fit, key=lambda v: (min(abs(ca(v)), abs(cb(v))), v.id))
+            order = sorted([v for v in rv if v is not inner], key=lambda v: (-abs(ca(v)), v.id)) + [inner]
             km = (order, ca(inner))
             kmulti = [(v.extent, ca(v), cb(v)) for v in order]
-        mm = _merge(mv, ca)
-        if mm is None:                                   # keep the densest one as m, batch the rest
-            inner = min(mv, key=lambda v: (abs(ca(v)), v.id))
-            bv += [v for v in mv if v is not inner]
-            mm = ([inner], ca(inner))
-        nm = _merge(nv, cb)
-        if nm is None:
-            inner = min(nv, key=lambda v: (abs(cb(v)), v.id))
-            bv += [v for v in nv if v is not inner]
-            nm = ([inner], cb(inner))
+        rows_multi = {}
+
+        def rows(vs, coef, which):
+            """vs as one row index: merged when their offsets form one linear index; else the
+            densest one, the rest batched; else, when that one is too narrow for a tile (the
+            positions of a convolution's output, a row of 24 in a plane of 26 x 26), all of them,
+            the operand's row offset then computed from each one's digit of the row index."""
+            mg = _merge(vs, coef)
+            if mg is not None:
+                return mg
+            inner = min(vs, key=lambda v: (abs(coef(v)), v.id))
+            if inner.extent >= MIN_SIDE:
+                bv.extend(v for v in vs if v is not inner)
+                return [inner], coef(inner)
+            rows_multi[which] = [(v.extent, coef(v)) for v in vs]
+            g = 0
+            for v in vs:
+                g = math.gcd(g, abs(coef(v)))
+            return list(vs), g
+        mm = rows(mv, ca, "a")
+        nm = rows(nv, cb, "b")
         s = GemmSpec()
         s.k, s.alpha = k, alpha
         s.ea, s.la, s.eb, s.lb = ea, la, eb, lb
@@ -180,6 +194,7 @@ def analyse(k: ir.Kernel):
         s.B = ir.prod(v.extent for v in s.batch)
         s.a_gather, s.b_gather = gathered_row(la), gathered_row(lb)
         s.k_multi = kmulti
+        s.a_multi, s.b_multi = rows_multi.get("a"), rows_multi.get("b")
         if (s.a_gather and (s.m_vars != [s.a_gather[2]] or s.batch or any(ca(v) for v in nv))) or \
                 (s.b_gather and (s.n_vars != [s.b_gather[2]] or s.batch or any(cb(v) for v in mv))):
             continue                                    # rows picked through an index: one plain row variable
@@ -207,6 +222,8 @@ def gathered_ok(s) -> bool:
         if g is not None and (s.K % 8 or ks != 1 or g[1] % 4 or not pipe):
             return False
     if s.k_multi and (not pipe or s.batch):
+        return False
+    if (s.a_multi or s.b_multi) and not pipe:
         return False
     return True
 
@@ -367,12 +384,24 @@ def follower_map(k: ir.Kernel, e: ir.Kernel):
         return None
     if ke == ee:
         return {ev: ir.Affine.of(kv) for ev, kv in zip(e.domain, k.domain)}
-    if len(e.domain) == 1:
-        flat = ir.Affine(0)
-        for kv, st in zip(k.domain, ir.row_major_strides(ke)):
-            flat = flat + ir.Affine(0, {kv: st})
-        return {e.domain[0]: flat}
-    return None
+    # each of e's variables spans a run of k's (one flattened variable; or a product whose merged
+    # variables were split back out, an implicit convolution)
+    m, i = {}, 0
+    for ev in e.domain:
+        run, span = [], 1
+        while span < ev.extent and i < len(k.domain):
+            run.append(k.domain[i])
+            span *= k.domain[i].extent
+            i += 1
+        if span != ev.extent:
+            return None
+        aff = ir.Affine(0)
+        for kv, st in zip(run, ir.row_major_strides([v.extent for v in run])):
+            aff = aff + ir.Affine(0, {kv: st})
+        m[ev] = aff
+    if any(v.extent != 1 for v in k.domain[i:]):
+        return None
+    return m
 
 
 def follower(k: ir.Kernel, e: ir.Kernel, hosts: set):
@@ -456,7 +485,7 @@ class GemmPlan(Plan):
             else:
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.waves, self.unroll = int(parts[1]), int(parts[2])
-        if s.a_gather or s.b_gather or s.k_multi:       # the pipelined K split only
+        if s.a_gather or s.b_gather or s.k_multi or s.a_multi or s.b_multi:     # the pipelined K split only
             self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
         self.pipe = self.pipe and self.sched == "ksplit" and not self.slab
         # K split across workgroups as well, when the output has few tiles and K is long (a
@@ -517,9 +546,18 @@ class GemmPlan(Plan):
     def grid(self):
         return (self.tn, self.tm, self.s.B * self.kslices), self.threads
 
-    def row_fn(self, sc, name, gather, rs) -> str:
-        """A device lambda: where row t of an operand starts (t·rs, or c·idx[t + ...] for a gathered
-        row, with the gather's bounds check)."""
+    def row_fn(self, sc, name, gather, rs, multi=None) -> str:
+        """A device lambda: where row t of an operand starts (t·rs; c·idx[t + ...] for a gathered
+        row, with the gather's bounds check; or, for rows over several variables, the sum of each
+        one's coefficient times its digit of t)."""
+        if multi:
+            parts, rest = [], "(uint32_t)t"
+            for depth, (ext, c) in enumerate(reversed(multi)):
+                idx = rest if depth == len(multi) - 1 else f"({rest} % {ext}u)"
+                if c:
+                    parts.append(f"{c}LL * (long long){idx}")
+                rest = f"({rest} / {ext}u)"
+            return f"    auto {name} = [=](int t) -> long long {{ return {' + '.join(parts) or '0LL'}; }};"
         if gather is None:
             return f"    auto {name} = [=](int t) -> long long {{ return (long long)t * {rs}LL; }};"
         g, c, v = gather
@@ -675,7 +713,8 @@ class GemmPlan(Plan):
                         f"    anvil_mm_tile_kslab<{self.amode}, {self.bmode}, {self.slab}, {chk(s.M)}, {chk(s.N)}>"
                         f"(part, {kargs});"]
             elif self.pipe:
-                body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs), self.row_fn(sc, "brow", s.b_gather, s.b_rs),
+                body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs, s.a_multi),
+                         self.row_fn(sc, "brow", s.b_gather, s.b_rs, s.b_multi),
                          self.k_fn("ak", "a"), self.k_fn("bk", "b")]
                 if self.kslices > 1:
                     krange = (f"(int)slice * {self.kslice}, min({self.kslice}, {s.K} - (int)slice * {self.kslice})")

@@ -250,6 +250,12 @@ class Plan:
         return "\n".join([f"__global__ void __launch_bounds__({threads}) {self.name}({self.params()}) {{"]
                          + self.host_prologue())
 
+    def sole_writer(self, k: ir.Kernel, st) -> bool:
+        """Is `st` the only store of this launch to its buffer that can reach a given element, so
+        that its `+=` needs no atomic? (Other kernels of the plan must not write the buffer.)"""
+        return A.sole_writer(k, st) and not any(
+            o.buf.root is st.buf.root for k2 in self.kernels if k2 is not k for o in k2.stores)
+
     # body helpers
     def statements(self, em: Emitter, k: ir.Kernel, scope: KernelScope, parallel: bool, guard: str | None = None,
                    on_store=None) -> None:
@@ -266,7 +272,7 @@ class Plan:
             off = em.affine(st.offset, st.buf)
             target = f"{scope.buf(st.buf)}[{off}]"
             if st.accumulate:
-                if parallel:
+                if parallel and not self.sole_writer(k, st):
                     line = f"atomicAdd(&{target}, {val});"
                 elif st.buf.dtype == I32:
                     line = f"{target} = anvil_wrap_add({target}, {val});"
@@ -321,6 +327,133 @@ class MapPlan(Plan):
 
     def grid(self):
         return self.blocks, self.threads
+
+
+# ----------------------------------------------------------------------------- gather-sum
+
+def scatter_targets(k: ir.Kernel):
+    """For an elementwise kernel whose one store adds (`+=`) to elements that several domain points
+    share, as the gradient of an im2col copy does (dX[n, c, i+u, j+v] += dP[n, i, j, c, u, v]):
+    (targets, summed vars) or None. Domain variables with the same coefficient in the store's
+    offset form one target coordinate y = their sum (extent: the sum of their extents less one
+    each), of which the widest member is then solved for (i = y - u); variables with coefficient 0
+    are summed whole. targets: (coefficient, extent, members, solved member) per coordinate, outer
+    to inner; None unless distinct coordinates reach distinct elements."""
+    if k.red is not None or k.uses_rand() or not k.domain or len(k.stores) != 1:
+        return None
+    st = k.stores[0]
+    if not st.accumulate or st.buf.dtype != F32 or any(not isinstance(t, Var) for t in st.offset.terms):
+        return None
+    if any(ld.buf.root is st.buf.root for ld in A.kernel_loads(k)):
+        return None
+    groups: dict = {}
+    free = []
+    for v in k.domain:
+        if v.extent <= 1:
+            continue
+        c = st.offset.coef(v)
+        if c == 0:
+            free.append(v)
+        else:
+            groups.setdefault(c, []).append(v)
+    if not free and all(len(g) == 1 for g in groups.values()):
+        return None
+    targets = []
+    for c, g in groups.items():
+        if len(g) == 1:
+            targets.append((c, g[0].extent, g, None))
+        else:
+            solved = max(g, key=lambda v: (v.extent, k.domain.index(v)))
+            targets.append((c, sum(v.extent - 1 for v in g) + 1, g, solved))
+    reach = 0
+    for c, ext, _, _ in sorted(targets, key=lambda t: abs(t[0])):
+        if abs(c) <= reach:
+            return None
+        reach += abs(c) * (ext - 1)
+    solved = {t[3] for t in targets if t[3] is not None}
+    summed = [v for v in k.domain if v.extent > 1 and (v in free or (st.offset.coef(v) and v not in solved
+                                                                       and len(groups[st.offset.coef(v)]) > 1))]
+    # lanes step along the coordinate the loads are densest in (they carry the traffic: each target
+    # element takes several loads); the rest outer to inner as the store's offset runs
+    targets.sort(key=lambda t: -abs(t[0]))
+    loads = A.kernel_loads(k)
+
+    def load_stride(t):
+        v = t[3] if t[3] is not None else t[2][0]
+        return sum(abs(ld.offset.coef(v)) for ld in loads)
+    dense = [t for t in targets if load_stride(t)]
+    if dense:
+        inner = min(dense, key=load_stride)
+        targets = [t for t in targets if t is not inner] + [inner]
+    return targets, summed
+
+
+class GatherSumPlan(Plan):
+    """The scatter of a `+=` kernel turned into a gather: one lane per element of the target
+    region, which loops over the domain points that add to it (in the domain's own order, so each
+    element takes the same additions in the same order as the sequential `+=`), skips those whose
+    solved variable falls outside its range, and writes the element once. No atomics, and every
+    element is read and written once."""
+
+    kind = "gather-sum"
+
+    def __init__(self, gen, k, name, targets, summed):
+        super().__init__(gen, [k], name)
+        self.k = k
+        self.targets, self.summed = targets, summed
+        self.total = ir.prod(t[1] for t in targets)
+        self.blocks = max(1, min(-(-self.total // THREADS), MAX_BLOCKS))
+
+    def source(self) -> str:
+        k, st = self.k, self.k.stores[0]
+        it = index_type(self.total)
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(k)
+        body: list[str] = []
+        em = Emitter(sc, body, "        ")
+        ys = [ir.Var(f"y{i}", t[1], id=900_000_000 + i) for i, t in enumerate(self.targets)]
+        for line in decode(ys, "w", it):
+            em.emit(line)
+        for y, (_, _, members, solved) in zip(ys, self.targets):
+            if solved is None:
+                em.emit(f"const int v{members[0].id} = v{y.id};")
+        for v in k.domain:
+            if v.extent <= 1:
+                em.emit(f"const int v{v.id} = 0;")
+        off = ir.Affine(st.offset.const, {y: t[0] for y, t in zip(ys, self.targets)})
+        target = f"{sc.buf(st.buf)}[{em.affine(off, st.buf)}]"
+        em.emit(f"float acc = {target};")
+        saved = em.memo
+        em.memo = dict(saved)
+        bound = set()
+        for v in self.summed:
+            em.emit(f"for (int v{v.id} = 0; v{v.id} < {v.extent}; v{v.id}++) {{")
+            em.ind += "    "
+            bound.add(v)
+            for y, (_, ext, members, solved) in zip(ys, self.targets):
+                if solved is None or v not in members or any(m not in bound for m in members if m is not solved):
+                    continue
+                rest = " - ".join([f"v{y.id}"] + [f"v{m.id}" for m in members if m is not solved])
+                em.emit(f"const int v{solved.id} = {rest};")
+                em.emit(f"if ((unsigned)v{solved.id} >= {solved.extent}u) continue;")
+        for stmt in k.stmts:
+            if isinstance(stmt, ir.Let):
+                em.let(stmt)
+            else:
+                em.emit(f"acc += {em.store_value(stmt)};")
+        for _ in self.summed:
+            em.ind = em.ind[:-4]
+            em.emit("}")
+        em.memo = saved
+        em.emit(f"{target} = acc;")
+        head = [self.comment() + " · the scatter as a gather: one lane per target element",
+                self.header(THREADS),
+                f"    for ({it} w = ({it})blockIdx.x * {THREADS}u + threadIdx.x; w < {self.total}u; "
+                f"w += ({it})gridDim.x * {THREADS}u) {{"]
+        return "\n".join(head + body + ["    }", "}"])
+
+    def grid(self):
+        return self.blocks, THREADS
 
 
 # ----------------------------------------------------------------------------- serial
