@@ -304,6 +304,9 @@ class HipGen:
                 if os.environ.get("ANVIL_GEMM_FUSE", "1") == "0" or self.check:   # no epilogue fusion
                     return g, 1
                 return g, 1 + self.absorb_followers(g, stmts, i + 1)
+        sl = HK.slice_count(k, self.emulate)
+        if sl > 1:
+            return HK.SlicePlan(self, k, name, sl), 1
         ty = HK.split_ways(k, self.emulate)
         if ty > 1:
             return HK.SplitPlan(self, k, name, ty), 1
@@ -333,8 +336,7 @@ class HipGen:
         The scan may cross one `if (host scalar) break;` (a step limit checked after the batch is
         gathered): the launch then goes after the check, and the leaving path launches the parts
         that came before the check on their own, so they run exactly when they did."""
-        if (self.emulate or self.check or os.environ.get("ANVIL_HIP_SIDE", "1") == "0"
-                or getattr(plan, "kslices", 1) > 1):
+        if self.emulate or self.check or os.environ.get("ANVIL_HIP_SIDE", "1") == "0":
             return plan, used
         ids = lambda bs: {b.root.id for b in bs}
 
@@ -368,8 +370,10 @@ class HipGen:
                 j += 1
                 continue
             cand, cused = self.plan_run(stmts, j)
-            if cand.kind in ("serial", "fused") or getattr(cand, "kslices", 1) > 1:
+            if cand.kind in ("serial", "fused"):
                 break
+            if getattr(cand, "kslices", 1) > 1 and exit_at is not None:
+                break                                   # its second launch follows the fused one
             moved = between + list(getattr(cand, "hoisted", []))
             if {st2.buf.root.id for h in moved for st2 in h.stores} & reads:
                 break
@@ -398,6 +402,8 @@ class HipGen:
             writes |= cw
             j += cused
             taken = j - i
+        if exit_at is not None and any(getattr(p, "kslices", 1) > 1 for p in parts):
+            return plan, used                           # the leaving path would need the second launch too
         if exit_at is not None and len(parts) == exit_at[1]:
             hoisted = exit_at[2]                        # nothing joined past the check: stop before it
             exit_at = None
@@ -555,7 +561,7 @@ class HipGen:
                 seg.append(("launch", self.launch(plan, ind), plan))
                 if getattr(plan, "kslices", 1) > 1:           # a K split across workgroups: its sum
                     if not hasattr(plan, "reduce_plan"):
-                        plan.reduce_plan = self.gemm.GemmReducePlan(plan)
+                        plan.reduce_plan = plan.second()
                         self.plans.append(plan.reduce_plan)
                     seg.append(("launch", self.launch(plan.reduce_plan, ind), plan.reduce_plan))
                 if self.check:

@@ -155,26 +155,28 @@ def rewrite(c: ir.Kernel, cp):
         return operand if isinstance(x, Load) and x.buf.root is dst else x
     c3 = dataclasses.replace(c2, red=dataclasses.replace(c2.red, body=ir.map_expr(c2.red.body, fn)))
     s = hip_gemm.analyse(c3)
-    if s is None or not hip_gemm.gathered_ok(s):
-        return None
-    if s.M * s.N * s.K < hip_gemm.MIN_WORK or min(s.M, s.N) < hip_gemm.MIN_SIDE:
+    if s is None or not hip_gemm.qualifies(s):
         return None
     return c3
 
 
 def forward_im2col_copies(prog: ir.Program) -> ir.Program:
     """Each product that reads an im2col copy's output reads the copy's source instead (see the
-    module docstring); a copy whose output then has no reader is dropped."""
+    module docstring), when every reader of the copy's output can, and the copy is dropped. (One
+    product left reading patches keeps the copy, and then the products over patches, with one
+    linear k, are the better ones.)"""
     rewritten: list = []
+    readers = A.all_readers(prog)
 
     def block(blk: ir.Block) -> ir.Block:
         out = [stmt(st) for st in blk.stmts]
         for i, st in enumerate(out):
             cp = im2col_copy(st)
-            if cp is None:
+            if cp is None or cp[1].kind not in A.SHARED_KINDS:
                 continue
             pk, dst, _, src = cp
             guard = {dst.id, src.buf.root.id}
+            new = {}
             for j in range(i + 1, len(out)):
                 s2 = out[j]
                 if isinstance(s2, ir.If) and not A.block_writes(s2.then) and not A.block_writes(s2.orelse):
@@ -186,11 +188,15 @@ def forward_im2col_copies(prog: ir.Program) -> ir.Program:
                 c = s2.kernel
                 if dst.id in {x.id for x in A.kernel_reads(c)}:
                     k2 = rewrite(c, cp)
-                    if k2 is not None:
-                        out[j] = dataclasses.replace(s2, kernel=k2)
-                        rewritten.append(dst)
-                if guard & {x.id for x in A.kernel_writes(out[j].kernel)}:
+                    if k2 is None:
+                        break
+                    new[j] = dataclasses.replace(s2, kernel=k2)
+                if guard & {x.id for x in A.kernel_writes(c)}:
                     break
+            if new and len(new) == readers.get(dst.id, 0):
+                for j, s2 in new.items():
+                    out[j] = s2
+                rewritten.append(dst)
         return dataclasses.replace(blk, stmts=out)
 
     def stmt(st):

@@ -150,9 +150,9 @@ def analyse(k: ir.Kernel):
             # K over several variables that are not one linear index of both operands (a weight
             # gradient summed over the batch and a convolution's positions, or a convolution's
             # channels and window): k decomposes over them, outer to inner; the innermost is the
-            # most contiguous of those whose extent is a multiple of 8 (a pipelined chunk of 8 k
-            # never straddles two of its runs)
-            fit = [v for v in rv if v.extent % 8 == 0]
+            # most contiguous of those whose extent is a multiple of 4 (the 4 consecutive k a lane
+            # loads at once never straddle two of its runs)
+            fit = [v for v in rv if v.extent % 4 == 0]
             if not fit:
                 continue
             inner = min(fit, key=lambda v: (min(abs(ca(v)), abs(cb(v))), v.id))
@@ -228,6 +228,17 @@ def gathered_ok(s) -> bool:
     return True
 
 
+def qualifies(s) -> bool:
+    """Is the product worth the matrix cores? Enough work, and both sides at least a tile wide;
+    a narrower one (a convolution's 32 x 9 weight gradient) only when K is long enough to be split
+    across workgroups, each reading its slice of both operands once."""
+    if s.M * s.N * s.K < MIN_WORK or not gathered_ok(s):
+        return False
+    if min(s.M, s.N) >= MIN_SIDE:
+        return True
+    return min(s.M, s.N) >= 8 and s.K >= 16384 and s.K % 8 == 0 and not s.batch
+
+
 def match(gen, k: ir.Kernel, name: str):
     """A GemmPlan for a contraction kernel (its stores may add to their buffer, `+=`: a gradient
     that collects several products; the epilogue then adds atomically, as the reference's parallel
@@ -235,7 +246,7 @@ def match(gen, k: ir.Kernel, name: str):
     if gen.emulate:
         return None
     s = analyse(k)
-    if s is None or s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < MIN_SIDE or not gathered_ok(s):
+    if s is None or not qualifies(s):
         return None
     return GemmPlan(gen, k, name, s)
 
@@ -320,9 +331,7 @@ def forward_gather_copies(prog: ir.Program, hosts: set) -> ir.Program:
         if any(ld.buf.root is dst for ld in A.kernel_loads(k2)):
             return None                                   # still reads the batch buffer elsewhere
         s = analyse(k2)
-        if s is None or not (s.a_gather or s.b_gather) or not gathered_ok(s):
-            return None
-        if s.M * s.N * s.K < MIN_WORK or min(s.M, s.N) < MIN_SIDE:
+        if s is None or not (s.a_gather or s.b_gather) or not qualifies(s):
             return None
         return k2
 
@@ -485,7 +494,8 @@ class GemmPlan(Plan):
             else:
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.waves, self.unroll = int(parts[1]), int(parts[2])
-        if s.a_gather or s.b_gather or s.k_multi or s.a_multi or s.b_multi:     # the pipelined K split only
+        if (s.a_gather or s.b_gather or s.k_multi or s.a_multi or s.b_multi
+                or min(s.M, s.N) < MIN_SIDE):                   # the pipelined K split only
             self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
         self.pipe = self.pipe and self.sched == "ksplit" and not self.slab
         # K split across workgroups as well, when the output has few tiles and K is long (a
@@ -599,6 +609,10 @@ class GemmPlan(Plan):
                 parts.append(f"{st}LL * (long long){idx}")
             rest = f"({rest} / {ext})"
         return f"    auto {name} = [=](int k) -> long long {{ return {' + '.join(parts) or '0LL'}; }};"
+
+    def second(self):
+        """The launch that adds the partial tiles of a K split across workgroups."""
+        return GemmReducePlan(self)
 
     def ws_buffer(self):
         """The partial tiles of a K split across workgroups: [slice][batch][M][N] floats."""

@@ -1203,6 +1203,13 @@ class FusedPlan(Plan):
         self.hoisted = hoisted
         for p in parts:
             self.skip_stores |= p.skip_stores
+        # parts that finish in a second launch (partial tiles or slices, then their sum): those
+        # second launches follow this one, side by side in turn
+        self.kslices = max(getattr(p, "kslices", 1) for p in parts)
+
+    def second(self):
+        seconds = [p.second() for p in self.parts if getattr(p, "kslices", 1) > 1]
+        return seconds[0] if len(seconds) == 1 else FusedPlan(self.gen, seconds, self.name + "r", [])
 
     @staticmethod
     def dims(p):
@@ -1307,6 +1314,123 @@ def split_ways(k: ir.Kernel, emulate: bool) -> int:
         if n >= 16 * ty:
             return ty
     return 1
+
+
+# ----------------------------------------------------------------------------- slices
+
+def slice_count(k: ir.Kernel, emulate: bool) -> int:
+    """S for a reduction with few outputs and a long, contiguous sum (a convolution's bias or weight
+    gradient: 32 outputs of 86528 terms), reduced in S slices per output by as many workgroups and
+    the slices then added in order (the reference's two-pass split, cuda.py:282-345); 1: not so."""
+    if emulate or k.red is None or k.red.op not in RED_CODE or k.uses_rand() or not k.domain:
+        return 1
+    n = ir.prod(v.extent for v in k.red.vars)
+    R = ir.prod(v.extent for v in k.domain)
+    if R > 1024 or n < 8192 or not inner_contiguous(k):
+        return 1
+    S = max(2, min(2048 // R, n // 2048))
+    return S if R * S <= MAX_BLOCKS else 1
+
+
+class SlicePlan(Plan):
+    """Workgroup (r, s) reduces slice s of output r's terms (256 lanes, then across the workgroup)
+    into partial[s][r]; SliceSumPlan, the next launch, adds each output's S partials in slice order
+    (the result does not depend on timing) and runs the kernel's statements."""
+
+    kind = "slices"
+
+    def __init__(self, gen, k, name, S):
+        super().__init__(gen, [k], name)
+        self.k = k
+        self.R = ir.prod(v.extent for v in k.domain)
+        self.n = ir.prod(v.extent for v in k.red.vars)
+        self.kslices = S
+        self.chunk = -(-self.n // S)
+
+    def ws_buffer(self):
+        """The partials, [slice][output]."""
+        if not hasattr(self, "_ws"):
+            self._ws = ir.Buffer(f"{self.name}.partials", (self.kslices * self.R,), self.k.red.body.dtype,
+                                 "scratch", id=810_000_000 + self.k.id)
+        return self._ws
+
+    def second(self):
+        return SliceSumPlan(self)
+
+    def source(self) -> str:
+        k, red = self.k, self.k.red
+        T, dt = ctype(red.body.dtype), red.body.dtype
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(k)
+        body: list[str] = []
+        em = Emitter(sc, body, "    ")
+        em.emit(f"__shared__ {T} sv[4];")
+        em.emit(f"const uint32_t r = blockIdx.x % {self.R}u, s = blockIdx.x / {self.R}u;")
+        for line in decode(k.domain, "r", "uint32_t"):
+            em.emit(line)
+        em.emit(f"{T} acc = {red_init(red.op, dt)};")
+        em.emit(f"const uint32_t jb = s * {self.chunk}u, je = min({self.n}u, jb + {self.chunk}u);")
+        em.emit("#pragma unroll 4")
+        em.emit("for (uint32_t j = jb + threadIdx.x; j < je; j += 256u) {")
+        em.ind += "    "
+        saved = em.memo
+        em.memo = dict(saved)
+        for line in decode(list(red.vars), "j", "uint32_t"):
+            em.emit(line)
+        val = em.ex(red.body)
+        em.emit(f"acc = {red_combine(red.op, dt, 'acc', val)};")
+        em.memo = saved
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        em.emit(f"acc = anvil_block_all<{RED_CODE[red.op]}, {T}>(acc, sv);")
+        em.emit(f"if (threadIdx.x == 0) {sc.buf(self.ws_buffer())}[s * {self.R}u + r] = acc;")
+        head = [self.comment() + f" · {self.R} outputs x {self.kslices} slices of {self.chunk}, added by "
+                f"{self.name}s", self.header(THREADS)]
+        return "\n".join(head + body + ["}"])
+
+    def grid(self):
+        return self.R * self.kslices, THREADS
+
+
+class SliceSumPlan(Plan):
+    """The second launch of a sliced reduction: each output's partials added in slice order, then
+    the kernel's statements with that sum as the reduction's value."""
+
+    kind = "slices-sum"
+
+    def __init__(self, first: SlicePlan):
+        super().__init__(first.gen, [], first.name + "s")
+        self.first = first
+        self.label = "slice sum + " + first.label
+        self.blocks = max(1, min(-(-first.R // THREADS), MAX_BLOCKS))
+        self.streams = list(first.streams)
+
+    def source(self) -> str:
+        f, k = self.first, self.first.k
+        red = k.red
+        T, dt = ctype(red.body.dtype), red.body.dtype
+        self.skip_stores = f.skip_stores
+        sc = KernelScope(self)
+        sc.stream_name = f.stream_param(k)
+        ws = sc.buf(f.ws_buffer())
+        body: list[str] = []
+        em = Emitter(sc, body, "        ")
+        em.emit(f"{T} sum = {ws}[e];")
+        em.emit(f"for (uint32_t sl = 1; sl < {f.kslices}u; sl++) "
+                f"sum = {red_combine(red.op, dt, 'sum', f'{ws}[sl * {f.R}u + e]')};")
+        for line in decode(k.domain, "e", "uint32_t"):
+            em.emit(line)
+        sc.acc_name = "sum"
+        sc.rand = "e"
+        self.statements(em, k, sc, parallel=True)
+        head = [f"// slices-sum: {f.name}: the {f.kslices} partials of each of {f.R} outputs added in order, "
+                "then the kernel's statements", self.header(THREADS),
+                f"    for (uint32_t e = blockIdx.x * {THREADS}u + threadIdx.x; e < {f.R}u; "
+                f"e += gridDim.x * {THREADS}u) {{"]
+        return "\n".join(head + body + ["    }", "}"])
+
+    def grid(self):
+        return self.blocks, THREADS
 
 
 # ----------------------------------------------------------------------------- row groups
