@@ -247,7 +247,8 @@ class HipGen:
             at = hip_attn.match(self, stmts, i)
             if at is not None:
                 return at, 6
-        got = self.row_block(stmts, i)
+        from . import hip_conv
+        got = hip_conv.match_dgrad(self, stmts, i) or self.row_block(stmts, i)
         if got is not None:
             return got
         return self.plan_one(stmts, i)

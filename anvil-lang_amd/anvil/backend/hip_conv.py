@@ -16,10 +16,13 @@ copy is not run at all: the 85 MB patches tensor of the CNN's second convolution
 from __future__ import annotations
 
 import dataclasses
+import os
 
 from .. import ir
 from ..ir import KernelStmt, Load, Var
 from . import hip_analysis as A
+from .hip_emit import flit
+from .hip_kernels import KernelScope, Plan
 
 
 def subst_affine(a: ir.Affine, m: dict) -> ir.Affine:
@@ -230,3 +233,241 @@ def forward_im2col_copies(prog: ir.Program) -> ir.Program:
             return dataclasses.replace(st, then=drop(st.then), orelse=drop(st.orelse))
         return st
     return dataclasses.replace(prog, main=drop(prog.main))
+
+
+# ----------------------------------------------------------------------------- the input gradient
+
+def _acc_store(k: ir.Kernel):
+    """k's one statement, a store of its sum (no epilogue), into a buffer it fills row-major."""
+    if k.red is None or k.red.op != "sum" or len(k.stmts) != 1 or not isinstance(k.stmts[0], ir.Store):
+        return None
+    st = k.stmts[0]
+    if st.accumulate or not isinstance(st.value, ir.Acc):
+        return None
+    strides = ir.row_major_strides([v.extent for v in k.domain])
+    want = ir.Affine(0, {v: s for v, s in zip(k.domain, strides) if v.extent > 1})
+    if st.offset != want or st.buf.root.numel != ir.prod(v.extent for v in k.domain):
+        return None
+    return st
+
+
+def _zero_fill(k: ir.Kernel, buf) -> bool:
+    """Does k set every element of buf to 0 (and do nothing else)?"""
+    if k.red is not None or len(k.stmts) != 1 or not isinstance(k.stmts[0], ir.Store) or not k.domain:
+        return False
+    st = k.stmts[0]
+    if st.buf.root is not buf or st.accumulate or not isinstance(st.value, ir.Const) or float(st.value.value) != 0.0:
+        return False
+    strides = ir.row_major_strides([v.extent for v in k.domain])
+    want = ir.Affine(0, {v: s for v, s in zip(k.domain, strides) if v.extent > 1})
+    return st.offset == want and buf.numel == ir.prod(v.extent for v in k.domain)
+
+
+def _digits(vs, src: str) -> dict:
+    """C expressions of each variable's digit of the row-major index src over vs (outer to inner)."""
+    out, rest = {}, f"(uint32_t)({src})"
+    for depth, v in enumerate(reversed(vs)):
+        out[v] = rest if depth == len(vs) - 1 else f"({rest} % {v.extent}u)"
+        rest = f"({rest} / {v.extent}u)"
+    return out
+
+
+def _offset_fn(vs, coef, src: str) -> str:
+    d = _digits(vs, src)
+    parts = [f"{coef(v)}LL * (long long){d[v]}" for v in vs if coef(v)]
+    return " + ".join(parts) or "0LL"
+
+
+def match_dgrad(gen, stmts: list, i: int):
+    """(DgradPlan, statements it takes) for a product that fills im2col-shaped gradients
+    dP[n, i, j, c, u, v] = Σ_o dY[n, o, i, j]·W[o, c, u, v], an optional zero fill of dX, and the
+    scatter dX[n, c, i+u, j+v] += dP[...] that is dP's only reader; else None."""
+    from . import hip_gemm
+    from .hip_kernels import scatter_targets
+    if gen.emulate or gen.check or os.environ.get("ANVIL_HIP_DGRAD", "1") == "0":
+        return None
+    if i + 1 >= len(stmts) or not isinstance(stmts[i], KernelStmt):
+        return None
+    G = stmts[i].kernel
+    gst = _acc_store(G)
+    if gst is None:
+        return None
+    dP = gst.buf.root
+    if dP.kind not in A.SHARED_KINDS or gen.readers.get(dP.id, 0) != 1:
+        return None
+    s = hip_gemm.analyse(G)
+    if s is None:
+        return None
+    zero, j = None, i + 1
+    if (j + 1 < len(stmts) and isinstance(stmts[j], KernelStmt) and isinstance(stmts[j + 1], KernelStmt)
+            and stmts[j].kernel.stores and not stmts[j].kernel.red):
+        zero = stmts[j].kernel
+        j += 1
+    if not isinstance(stmts[j], KernelStmt):
+        return None
+    S = stmts[j].kernel
+    if (len(S.stmts) != 1 or not isinstance(S.stmts[0], ir.Store) or not isinstance(S.stmts[0].value, Load)
+            or S.stmts[0].value.buf.root is not dP):
+        return None
+    sst = S.stmts[0]
+    dX = sst.buf.root
+    scat = scatter_targets(S)
+    if scat is None or dX.id in {b.id for b in A.kernel_reads(G)}:
+        return None
+    if zero is not None and not _zero_fill(zero, dX):
+        return None
+    targets, summed = scat
+    # dP's element as S reads it, in G's variables: each of G's (merged) variables is a mixed-radix
+    # number over S's variables
+    loff = sst.value.offset
+    if loff.const or any(not isinstance(t, Var) for t in loff.terms):
+        return None
+    gmap, claimed = {}, set()
+    for g, st_g in zip(G.domain, ir.row_major_strides([v.extent for v in G.domain])):
+        mine = sorted([v for v in S.domain if v.extent > 1 and st_g <= loff.coef(v) < st_g * g.extent
+                       and loff.coef(v) % st_g == 0], key=lambda v: loff.coef(v))
+        span, aff = 1, ir.Affine(0)
+        for v in mine:
+            if loff.coef(v) != st_g * span:
+                return None
+            aff = aff + ir.Affine(0, {v: span})
+            span *= v.extent
+        if span != g.extent and g.extent > 1:
+            return None
+        gmap[g] = aff
+        claimed.update(id(v) for v in mine)
+    if any(v.extent > 1 and id(v) not in claimed for v in S.domain):
+        return None
+    # the target coordinates: a solved variable i = y - u (others of its group)
+    tvars, rmap, preds = [], {}, []
+    for c, ext, members, solved in targets:
+        if solved is None:
+            tvars.append((members[0], c))
+            continue
+        y = Var(f"{solved.name}+", ext)
+        tvars.append((y, c))
+        rmap[solved] = ir.Affine.of(y) - sum((ir.Affine.of(m) for m in members if m is not solved), ir.Affine(0))
+        preds.append((solved, y, [m for m in members if m is not solved]))
+    ops = []
+    for e, ld in ((s.ea, s.la), (s.eb, s.lb)):
+        off1 = subst_affine(ld.offset, gmap)
+        if off1.gathers() or off1.scalars():
+            return None
+        off2 = subst_affine(off1, rmap)
+        ops.append((e, ld, off1, off2))
+    # which operand each coordinate, each k variable and each window check belongs to
+    side_pred = {0: [], 1: []}
+    for solved, y, others in preds:
+        users = [n for n in (0, 1) if ops[n][2].coef(solved)]
+        if len(users) != 1:
+            return None
+        side_pred[users[0]].append((solved, y, others))
+    rows = {0: [], 1: []}
+    for tv, c in sorted(tvars, key=lambda t: -abs(t[1])):
+        users = {n for n in (0, 1) if ops[n][3].coef(tv)} | {n for n in (0, 1) for _, y, _ in side_pred[n] if y is tv}
+        if len(users) != 1:
+            return None
+        rows[users.pop()].append(tv)
+    if not rows[0] or not rows[1]:
+        return None
+    innermost = min(tvars, key=lambda t: abs(t[1]))[0]
+    if innermost in rows[0]:                        # lanes step along dX's contiguous coordinate
+        ops.reverse()
+        rows = {0: rows[1], 1: rows[0]}
+        side_pred = {0: side_pred[1], 1: side_pred[0]}
+    kv = list(summed) + list(G.red.vars)
+    in_pred = {id(m) for n in (0, 1) for _, _, others in side_pred[n] for m in others}
+    coefs = lambda v: (ops[0][3].coef(v), ops[1][3].coef(v))
+    fit = [v for v in kv if v.extent % 4 == 0 and id(v) not in in_pred and any(coefs(v))]
+    if not fit or any(not any(coefs(v)) and id(v) not in in_pred for v in kv):
+        return None
+    inner = min(fit, key=lambda v: (min(abs(c) for c in coefs(v) if c), v.id))
+    korder = sorted([v for v in kv if v is not inner], key=lambda v: (-max(abs(c) for c in coefs(v)), v.id)) + [inner]
+    M = ir.prod(v.extent for v in rows[0])
+    N = ir.prod(v.extent for v in rows[1])
+    K = ir.prod(v.extent for v in kv)
+    if K % 8 or M < 8 or N < 32 or M * N * K < hip_gemm.MIN_WORK:
+        return None
+    plan = DgradPlan(gen, [G] + ([zero] if zero is not None else []) + [S], f"k{G.id}", G, S, zero is not None,
+                     s.alpha, ops, rows, korder, side_pred, tvars, sst, M, N, K)
+    return plan, j + 1 - i
+
+
+class DgradPlan(Plan):
+    """A convolution's input gradient in one pass over the matrix cores, without its im2col-shaped
+    intermediate: dX[n, c, y, x] (+)= Σ_{u, v, o} W[o, c, u, v]·dY[n, o, y-u, x-v], K running over the
+    window and the output channels; a window position that hangs over dY's edge (y-u outside
+    0..23) is not loaded and counts as zero, which is exactly the scatter's missing term. Each output
+    element is written once, by the lane that owns it (no atomics); when the zero fill of dX was part
+    of the run, the sum is stored over it. The terms add in the matrix cores' order rather than the
+    scatter's, as any product's do."""
+
+    kind = "conv-dgrad"
+
+    def __init__(self, gen, kernels, name, G, S, zeroed, alpha, ops, rows, korder, side_pred, tvars, sst, M, N, K):
+        super().__init__(gen, kernels, name)
+        self.G, self.S, self.zeroed, self.alpha = G, S, zeroed, alpha
+        self.ops, self.rows, self.korder, self.side_pred = ops, rows, korder, side_pred
+        self.tvars, self.sst, self.M, self.N, self.K = tvars, sst, M, N, K
+        self.skip_stores = {(k.id, 0) for k in kernels if k is not S}     # dP is never written; dX once
+        self.tm, self.tn = -(-M // 32), -(-N // 32)
+        nch = -(-(K // 8) // 4)
+        self.nch, self.depth = nch, min(2 if nch <= 32 else 4, nch)
+
+    def grid(self):
+        return (self.tn, self.tm, 1), 256
+
+    def source(self) -> str:
+        from . import hip_gemm
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(self.G)
+        body = []
+        names = ("a", "b")
+        for n in (0, 1):
+            e, ld, off1, off2 = self.ops[n]
+            body.append(hip_gemm.GemmPlan.operand(self, sc, e, ld, f"op{names[n]}"))
+        body += ["    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;"]
+        for n in (0, 1):
+            e, ld, off1, off2 = self.ops[n]
+            body.append(f"    const float *p{names[n]} = {sc.buf(ld.buf)} + ({off2.const}LL);")
+            body.append(f"    auto {names[n]}row = [=](int t) -> long long {{ return "
+                        f"{_offset_fn(self.rows[n], off2.coef, 't')}; }};")
+            body.append(f"    auto {names[n]}k = [=](int k) -> long long {{ return "
+                        f"{_offset_fn(self.korder, off2.coef, 'k')}; }};")
+            checks = []
+            if self.side_pred[n]:
+                td, kd = _digits(self.rows[n], "t"), _digits(self.korder, "k")
+                for solved, y, others in self.side_pred[n]:
+                    diff = " - ".join([f"(int){td[y]}"] + [f"(int){kd[m]}" for m in others])
+                    checks.append(f"(unsigned)({diff}) < {solved.extent}u")
+            if checks:
+                body.append(f"    auto {names[n]}pred = [=](int t, int k) -> bool {{ return {' && '.join(checks)}; }};")
+            else:
+                body.append(f"    anvil_all_pred {names[n]}pred;")
+        inner = self.korder[-1]
+        a_ks, b_ks = self.ops[0][3].coef(inner), self.ops[1][3].coef(inner)
+        chk = lambda x: "true" if x % 32 else "false"
+        body += ["    float part[1][1][4];",
+                 f"    anvil_mm_tile_kpipe<4, 1, 1, ANVIL_LD_ANY, ANVIL_LD_ANY, {self.nch}, {self.depth}, {chk(self.M)}, "
+                 f"{chk(self.N)}>(part, pa, arow, ak, {a_ks}LL, pb, brow, bk, {b_ks}LL, {self.M}, {self.N}, m0, n0, "
+                 f"0, {self.K}, opa, opb, apred, bpred);",
+                 "    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;",
+                 "#pragma unroll",
+                 "    for (int q = 0; q < 4; q++) {",
+                 "        const int vv = 4 * wave + q;",
+                 "        const int mi = m0 + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
+                 "        const int ni = n0 + (lane & 31);",
+                 f"        if (mi >= {self.M} || ni >= {self.N}) continue;"]
+        dm, dn = _digits(self.rows[0], "mi"), _digits(self.rows[1], "ni")
+        out = [str(self.sst.offset.const)] if self.sst.offset.const else []
+        for tv, c in self.tvars:
+            d = dm.get(tv, dn.get(tv))
+            out.append(f"{c}LL * (long long){d}")
+        target = f"{sc.buf(self.sst.buf)}[{' + '.join(out)}]"
+        base = "0.0f" if self.zeroed else target
+        body.append(f"        {target} = {base} + {flit(self.alpha)} * part[0][0][q];")
+        body.append("    }")
+        head = [f"// conv-dgrad: {self.G.name} (product into an im2col-shaped gradient) and {self.S.name} (its "
+                f"scatter) as one product · {self.M}x{self.N}x{self.K}, window terms over the edge skipped",
+                self.header(256)]
+        return "\n".join(head + body + ["}"])

@@ -276,8 +276,8 @@ __device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][16 / W
 // offsets; 4 consecutive k are a_ks (b_ks) apart. The workgroup covers k in [kbeg, kbeg + K).
 template <int MODE, bool CHK>
 __device__ __forceinline__ void anvil_chunk_load_k(float (&r)[4], const float *__restrict__ p, long long toff,
-                                                   long long koff, long long ks, int t, int tmax) {
-    if (CHK && t >= tmax) {
+                                                   long long koff, long long ks, int t, int tmax, bool ok = true) {
+    if ((CHK && t >= tmax) || !ok) {
         r[0] = r[1] = r[2] = r[3] = 0.f;
         return;
     }
@@ -293,13 +293,21 @@ __device__ __forceinline__ void anvil_chunk_load_k(float (&r)[4], const float *_
     }
 }
 
+// Which (row, k) operand elements exist: all of them, unless a product reads a window of its
+// operand that may hang over the edge (a convolution's input gradient: dY[y - u]); the 4
+// consecutive k a lane loads at once share the answer.
+struct anvil_all_pred {
+    __device__ __forceinline__ bool operator()(int, int) const { return true; }
+};
+
 template <int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, bool FULL, class AK, class BK,
-          class OPA, class OPB>
+          class OPA, class OPB, class APRED, class BPRED>
 __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
                                                     const float *__restrict__ a, const long long (&ao)[TM], AK ak,
                                                     long long a_ks, const float *__restrict__ b,
                                                     const long long (&bo)[TN], BK bk, long long b_ks,
-                                                    int M, int N, int m0, int n0, int c0, int n, OPA opa, OPB opb) {
+                                                    int M, int N, int m0, int n0, int c0, int n, OPA opa, OPB opb,
+                                                    APRED apred, BPRED bpred) {
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     float ab[D][TM][4], bb[D][TN][4];
 #define ANVIL_KP_LOAD(d, c)                                                                                \
@@ -307,9 +315,11 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
         const int k_ = 8 * (c0 + (c)) + 4 * h;                                                             \
         const long long ka_ = ak(k_), kb_ = bk(k_);                                                        \
         _Pragma("unroll") for (int i = 0; i < TM; i++)                                                     \
-            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, ao[i], ka_, a_ks, m0 + 32 * i + r, M);           \
+            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, ao[i], ka_, a_ks, m0 + 32 * i + r, M,            \
+                                            apred(m0 + 32 * i + r, k_));                                   \
         _Pragma("unroll") for (int j = 0; j < TN; j++)                                                     \
-            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, bo[j], kb_, b_ks, n0 + 32 * j + r, N);           \
+            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, bo[j], kb_, b_ks, n0 + 32 * j + r, N,            \
+                                            bpred(n0 + 32 * j + r, k_));                                   \
     }
 #pragma unroll
     for (int c = 0; c < D; c++) ANVIL_KP_LOAD(c, c)
@@ -333,11 +343,12 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
 }
 
 template <int W, int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, class AROW, class BROW,
-          class AK, class BK, class OPA, class OPB>
+          class AK, class BK, class OPA, class OPB, class APRED = anvil_all_pred, class BPRED = anvil_all_pred>
 __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W],
                                                     const float *__restrict__ a, AROW arow, AK ak, long long a_ks,
                                                     const float *__restrict__ b, BROW brow, BK bk, long long b_ks,
-                                                    int M, int N, int m0, int n0, int kbeg, int K, OPA opa, OPB opb) {
+                                                    int M, int N, int m0, int n0, int kbeg, int K, OPA opa, OPB opb,
+                                                    APRED apred = APRED(), BPRED bpred = BPRED()) {
     constexpr int PER = 16 / W;
     __shared__ float part[W * TM * TN * 16 * 64];
     const int lane = threadIdx.x & 63, r = lane & 31;
@@ -352,10 +363,10 @@ __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W]
     acc.zero();
     if (n == NCH)
         anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, true>(acc, a, ao, ak, a_ks, b, bo, bk, b_ks, M, N,
-                                                                            m0, n0, c0, n, opa, opb);
+                                                                            m0, n0, c0, n, opa, opb, apred, bpred);
     else if (n > 0)
         anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, false>(acc, a, ao, ak, a_ks, b, bo, bk, b_ks, M,
-                                                                             N, m0, n0, c0, n, opa, opb);
+                                                                             N, m0, n0, c0, n, opa, opb, apred, bpred);
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
