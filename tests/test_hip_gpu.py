@@ -55,6 +55,55 @@ def test_gpu_attention_at_full_size_matches_closed_form():
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
 
 
+def _full_size_call(name, args):
+    from anvil.hip_function import Compiled, Lowered
+    prog, data = load_ir(name)
+    low = Lowered.from_fixture(prog, data)
+    assert [tuple(b.shape) for b in low.inputs] == [a.shape for a in args]
+    return Compiled(low.name, low, seed=data.get("seed", 0)).call(args)
+
+
+def test_gpu_softmax_at_full_size_matches_closed_form():
+    """C3's softmax over the rows of [8192, 4096] (inputs ~N(0,1), seed 2) against float64 NumPy;
+    every row also sums to 1."""
+    print("gpu softmax full size", flush=True)
+    x = np.random.default_rng(2).standard_normal((8192, 4096)).astype(np.float32)
+    got = _full_size_call("c3_softmax", [x])
+    e = np.exp(x.astype(np.float64) - x.max(axis=1, keepdims=True))
+    want = e / e.sum(axis=1, keepdims=True)
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-7)
+    np.testing.assert_allclose(got.astype(np.float64).sum(axis=1), 1.0, rtol=0, atol=1e-4)
+
+
+def test_gpu_layernorm_at_full_size_matches_closed_form():
+    """C3's layer_norm(x)·γ + β at [8192, 1024] (eps 1e-5, biased variance) against float64 NumPy."""
+    print("gpu layernorm full size", flush=True)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((8192, 1024)).astype(np.float32)
+    g = rng.standard_normal(1024).astype(np.float32)
+    b = rng.standard_normal(1024).astype(np.float32)
+    got = _full_size_call("c3_layernorm", [x, g, b])
+    x64 = x.astype(np.float64)
+    mu = x64.mean(axis=1, keepdims=True)
+    var = ((x64 - mu) ** 2).mean(axis=1, keepdims=True)
+    want = (x64 - mu) / np.sqrt(var + 1e-5) * g + b
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4)
+
+
+def test_gpu_linear_at_full_size_matches_closed_form():
+    """C3's linear y = x·Wᵀ + b at [8192, 4096] × [4096, 4096] (the 128 x 128 tile schedule): one row
+    of each of the 64 row tiles, at a different place in each tile, against float64 NumPy."""
+    print("gpu linear full size", flush=True)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((8192, 4096)).astype(np.float32)
+    w = rng.standard_normal((4096, 4096)).astype(np.float32)
+    b = rng.standard_normal(4096).astype(np.float32)
+    got = _full_size_call("c3_linear", [x, w, b])
+    rows = 128 * np.arange(64) + (37 * np.arange(64)) % 128
+    want = x[rows].astype(np.float64) @ w.astype(np.float64).T + b
+    np.testing.assert_allclose(got[rows], want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
+
+
 def _source_lines(prog, data):
     from anvil.backend import hip
     return hip.generate(prog, seed=data.get("seed", 0), library=True).splitlines()
