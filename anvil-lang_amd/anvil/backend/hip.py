@@ -872,7 +872,7 @@ class HipGen:
         src = self.prog.source
         name = src.display_path() if src is not None and hasattr(src, "display_path") else "<program>"
         out = [f"// Generated by anvil (HIP backend) from {name} for MI355X ({ARCH}).",
-               f"// Build: hipcc --offload-arch={ARCH} -O3 -fPIC -shared -ffp-contract=off -munsafe-fp-atomics prog.hip -o prog.so -lz",
+               f"// Build: hipcc --offload-arch={ARCH} {' '.join(f for f in HIP_FLAGS if f != '-w')} prog.hip -o prog.so -lz",
                "", runtime_source(), "",
                "// ---------------------------------------------------------------- buffers"]
         for b in dev:
@@ -1073,8 +1073,12 @@ def hipcc() -> str:
     raise HipToolchainError("hipcc not found (ROCm is needed to build for MI355X; set $HIPCC)")
 
 
+# -amdgpu-mfma-vgpr-form: matrix-core accumulators in ordinary VGPRs. With the compiler's own choice
+# the attention kernel kept its output tiles in AGPRs and copied all 64 of them out and back on every
+# key tile around the (VALU) softmax rescale: 272 register moves per 128 MFMAs. No generated kernel
+# spills with it.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-munsafe-fp-atomics", "-w",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def build(source: str, lib_path: str, emulate: bool = False) -> None:

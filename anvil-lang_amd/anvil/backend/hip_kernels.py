@@ -278,6 +278,8 @@ class Plan:
                     line = f"{target} = anvil_wrap_add({target}, {val});"
                 else:
                     line = f"{target} += {val};"
+            elif st.buf.root.kind == "output" and st.buf.dtype == F32:
+                line = f"anvil_store_out(&{target}, {val});"
             else:
                 line = f"{target} = {val};"
             em.emit(f"if ({guard}) {line}" if guard else line)

@@ -531,16 +531,17 @@ __device__ __forceinline__ void anvil_mm_tile_kslab(float (&out)[1][1][4],
 
 // Attention without the score matrix: O[b] = softmax(scale · Q[b] K[b]ᵀ) V[b], rows of Q in 32-query
 // tiles, one tile per workgroup whose four wavefronts each take a quarter of the keys (32 at a time)
-// and are merged at the end. Everything is computed transposed, Sᵀ = K Qᵀ and Oᵀ = Vᵀ Pᵀ, so that
-// lane l always holds query l % 32 (half h = l / 32): its running max and sum are lane-local, and
-// the Sᵀ accumulators of lane l (keys 8(v/4) + 4h + v%4 of the tile) are exactly the Pᵀ operand
+// and are merged at the end (eight wavefronts, two per SIMD, measured 16 % slower). Everything is
+// computed transposed, Sᵀ = K Qᵀ and Oᵀ = Vᵀ Pᵀ, so that lane l always holds query l % 32 (half
+// h = l / 32): its running max and sum are lane-local, and the Sᵀ accumulators of lane l (keys 8(v/4) + 4h + v%4 of the tile) are exactly the Pᵀ operand
 // lane l must supply to the next MFMAs, taking key slot h of MFMA v; the Vᵀ operand follows the same
 // key order. Output rows d of the DT = D/32 Oᵀ tiles are interleaved, d = DT·i + j, so each lane
 // loads DT consecutive floats of a V row at once. Per key tile: running max m, p = 2^(s - m) with s
 // in base 2 (Q pre-scaled by scale · log2 e), l = l·c + Σp, O = O·c + Vᵀ p with c = 2^(m_old - m_new)
 // (the online softmax; the reference exponentiates s·scale - max in base e after the full row: the
-// same values up to rounding). O is rescaled only when some lane's maximum moved. Q stays in registers (D/2 floats per
-// lane); the next tile's K and V rows are loaded while the current one is multiplied.
+// same values up to rounding). O is rescaled only when some lane's maximum moved. The scaled query
+// tile sits in LDS, shared by the four waves (registers go to K, V and the accumulators); the next
+// tile's K and V rows are loaded while the current one is multiplied.
 template <int D>
 struct anvil_vec_of { typedef float type; };
 template <> struct anvil_vec_of<64> { typedef float __attribute__((ext_vector_type(2))) type; };
@@ -555,17 +556,19 @@ __device__ __forceinline__ void anvil_attention_tile(const float *__restrict__ q
     typedef typename anvil_vec_of<D>::type vec;
     __shared__ float part[4][DT][16][64];
     __shared__ float stat[4][2][32];
+    __shared__ float qsh[32][D + 4];            // the query tile, scaled: read by the four waves
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int per = Lk / 4, kb = w * per;
     // scores in base 2: Q is scaled once by scale · log2(e), and p = 2^(s - m) (v_exp_f32)
     const float qs = scale * 1.4426950408889634f;
-    float qr[DH];
-#pragma unroll
-    for (int s4 = 0; s4 < DH; s4 += 4) {
-        const anvil_f32x4 x = *(const anvil_f32x4 *)(q + (long long)(q0 + r) * D + DH * h + s4);
-        qr[s4] = x.x * qs; qr[s4 + 1] = x.y * qs; qr[s4 + 2] = x.z * qs; qr[s4 + 3] = x.w * qs;
+    for (int i = threadIdx.x; i < 32 * D / 4; i += 256) {
+        const int row = i / (D / 4), c4 = 4 * (i % (D / 4));
+        const anvil_f32x4 x = *(const anvil_f32x4 *)(q + (long long)(q0 + row) * D + c4);
+        qsh[row][c4] = x.x * qs; qsh[row][c4 + 1] = x.y * qs; qsh[row][c4 + 2] = x.z * qs; qsh[row][c4 + 3] = x.w * qs;
     }
+    __syncthreads();
+    const float *qrow = &qsh[r][DH * h];
     anvil_f32x16 oacc[DT];
 #pragma unroll
     for (int j = 0; j < DT; j++)
@@ -588,8 +591,10 @@ __device__ __forceinline__ void anvil_attention_tile(const float *__restrict__ q
         anvil_f32x16 sacc;
 #pragma unroll
         for (int e = 0; e < 16; e++) sacc[e] = 0.f;
+        int qo = 0;
+        asm volatile("" : "+v"(qo));            // read Q from LDS here, each tile: not kept in registers
 #pragma unroll
-        for (int s = 0; s < DH; s++) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[s], qr[s], sacc, 0, 0, 0);
+        for (int s = 0; s < DH; s++) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[s], qrow[s + qo], sacc, 0, 0, 0);
         if (k0 + 32 < kb + per) ANVIL_AT_LOADK(k0 + 32)
         float mx = -__builtin_inff();
 #pragma unroll
