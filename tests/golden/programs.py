@@ -455,6 +455,9 @@ PROGRAMS = [
      "function": {"name": "norm", "args": [([48, 200], "f32"), ([200], "f32"), ([200], "f32")]}},
     {"name": "c3_linear_small", "source": C3_LINEAR, "interp": True,
      "function": {"name": "linear", "args": [([96, 80], "f32"), ([72, 80], "f32"), ([72], "f32")]}},
+    # a product of 1024 x 1024 outputs over K = 512: the pipelined K split with 1024 tiles
+    {"name": "c3_linear_w2", "source": C3_LINEAR, "interp": True,
+     "function": {"name": "linear", "args": [([1024, 512], "f32"), ([1024, 512], "f32"), ([1024], "f32")]}},
     {"name": "c3_attention_small", "source": C3_ATTENTION, "interp": True,
      "function": {"name": "attention", "args": [([2, 64, 32], "f32")] * 3}},
     # shapes the one-kernel attention takes (head size 64 and 128, keys a multiple of 128)
