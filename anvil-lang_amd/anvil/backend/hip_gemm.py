@@ -146,6 +146,19 @@ def analyse(k: ir.Kernel):
             continue
         km = _merge(rv, ca, cb)
         kmulti = None
+        ktab = None
+        if km is None:
+            # K linear with unit stride in one operand (a convolution's weights over c, u, v) but not
+            # in the other (its input: 676c + 26u + v): k in the linear operand's order, and the other
+            # operand's offset of each k from a table
+            for which, lin_c, tab_c in (("b", ca, cb), ("a", cb, ca)):
+                lin = _merge(rv, lin_c)
+                K_ = ir.prod(v.extent for v in rv)
+                if lin is not None and abs(lin[1]) == 1 and K_ % 8 == 0 and K_ <= 4096:
+                    km = lin
+                    steps = [(v.extent, tab_c(v)) for v in lin[0]]
+                    ktab = (which, steps)
+                    break
         if km is None:
             # K over several variables that are not one linear index of both operands (a weight
             # gradient summed over the batch and a convolution's positions, or a convolution's
@@ -195,6 +208,20 @@ def analyse(k: ir.Kernel):
         s.a_gather, s.b_gather = gathered_row(la), gathered_row(lb)
         s.k_multi = kmulti
         s.a_multi, s.b_multi = rows_multi.get("a"), rows_multi.get("b")
+        s.a_ktab = s.b_ktab = None
+        if ktab is not None:
+            offs = [0] * s.K
+            strides = ir.row_major_strides([e for e, _ in ktab[1]])
+            for kk in range(s.K):
+                offs[kk] = sum(c * ((kk // st) % e) for (e, c), st in zip(ktab[1], strides))
+            if ktab[0] == "a":
+                s.a_ktab = offs
+            else:
+                s.b_ktab = offs
+            if ktab[0] == "b":
+                s.b_ks = 0
+            else:
+                s.a_ks, s.b_ks = 0, km[1]
         if (s.a_gather and (s.m_vars != [s.a_gather[2]] or s.batch or any(ca(v) for v in nv))) or \
                 (s.b_gather and (s.n_vars != [s.b_gather[2]] or s.batch or any(cb(v) for v in mv))):
             continue                                    # rows picked through an index: one plain row variable
@@ -223,7 +250,7 @@ def gathered_ok(s) -> bool:
             return False
     if s.k_multi and (not pipe or s.batch):
         return False
-    if (s.a_multi or s.b_multi) and not pipe:
+    if (s.a_multi or s.b_multi or s.a_ktab or s.b_ktab) and not pipe:
         return False
     return True
 
@@ -475,6 +502,10 @@ class GemmPlan(Plan):
         ca, cb = s.la.offset.coef, s.lb.offset.coef
         self.amode = load_mode(s.a_rs, s.a_ks, s.M, s.K, s.la.offset.const, [ca(v) for v in s.batch])
         self.bmode = load_mode(s.b_rs, s.b_ks, s.N, s.K, s.lb.offset.const, [cb(v) for v in s.batch])
+        if s.a_ktab:
+            self.amode = "ANVIL_LD_KT"
+        if s.b_ktab:
+            self.bmode = "ANVIL_LD_KT"
         self.slab = 0
         # tuning: $ANVIL_GEMM_FORCE = comma-separated "tile64" | "tile128" | "ksplit:W:U" | "slab:KC",
         # each optionally "@NN" / "@NT" / "@TN" (only products whose operands load that way)
@@ -494,7 +525,7 @@ class GemmPlan(Plan):
             else:
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.waves, self.unroll = int(parts[1]), int(parts[2])
-        if (s.a_gather or s.b_gather or s.k_multi or s.a_multi or s.b_multi
+        if (s.a_gather or s.b_gather or s.k_multi or s.a_multi or s.b_multi or s.a_ktab or s.b_ktab
                 or min(s.M, s.N) < MIN_SIDE):                   # the pipelined K split only
             self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
         self.pipe = self.pipe and self.sched == "ksplit" and not self.slab
@@ -593,10 +624,30 @@ class GemmPlan(Plan):
         sc.fwd, sc.canon = saved
         return "\n".join([f"    auto {name} = [=](float x) -> float {{"] + lines + [f"        return {v};", "    };"])
 
+    def k_table(self, which) -> str:
+        """The file-scope table of an operand's k offsets (one int per k), when it has one."""
+        tab = self.s.a_ktab if which == "a" else self.s.b_ktab
+        if not tab:
+            return ""
+        body = ", ".join(str(x) for x in tab)
+        return (f"static __device__ const int anvil_ktab_{self.name}_{which}[{len(tab)}] __attribute__((aligned(16))) "
+                f"= {{{body}}};\n")
+
     def k_fn(self, name, which) -> str:
         """A device lambda: where k-index k of an operand starts (k·stride, or the offsets of the
-        several K variables it decomposes into)."""
+        several K variables it decomposes into); for an operand with a table, an object that reads
+        the table (one k, or four consecutive ones at once)."""
         s = self.s
+        if (s.a_ktab if which == "a" else s.b_ktab):
+            t = f"anvil_ktab_{self.name}_{which}"
+            return "\n".join([
+                "    struct {",
+                f"        __device__ long long operator()(int k) const {{ return {t}[k]; }}",
+                "        __device__ void quad(int k, long long (&o)[4]) const {",
+                f"            const anvil_i32x4 q = *(const anvil_i32x4 *)({t} + k);",
+                "            o[0] = q.x; o[1] = q.y; o[2] = q.z; o[3] = q.w;",
+                "        }",
+                f"    }} {name};"])
         if not s.k_multi:
             ks = s.a_ks if which == "a" else s.b_ks
             return f"    auto {name} = [=](int k) -> long long {{ return (long long)k * {ks}LL; }};"
@@ -747,7 +798,7 @@ class GemmPlan(Plan):
                         f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]
             value = "part[0][0][q]"
         def head():                                   # after the body: its buffers are the parameters
-            return [self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
+            return [self.k_table("a") + self.k_table("b") + self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
                     + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, B {self.bmode[9:]}"
                     + (f" · K in {self.kslices} slices of {self.kslice}, partial tiles" if self.kslices > 1 else "")
                     + (f" · K over {len(s.k_multi)} variables" if s.k_multi else ""),

@@ -27,6 +27,25 @@ typedef float anvil_f32x4 __attribute__((ext_vector_type(4)));
 #define ANVIL_LD_KC 0        // contiguous along k
 #define ANVIL_LD_RC 1        // contiguous along the row / column index (m for A, n for B)
 #define ANVIL_LD_ANY 2       // neither: one element at a time
+#define ANVIL_LD_KT 3        // one element at a time, where each of 4 consecutive k starts is read from
+                             // a table (k over variables whose strides do not line up: a convolution's
+                             // input read as c, u, v while the weights run linearly over them)
+
+typedef int anvil_i32x4 __attribute__((ext_vector_type(4)));
+
+// The offsets of k .. k + 3 (k a multiple of 4) in an operand: kf(k) + s·ks, or four table entries.
+template <int MODE, class KF>
+__device__ __forceinline__ void anvil_koffs(KF kf, int k, long long ks, long long (&o)[4]) {
+    if constexpr (MODE == ANVIL_LD_KT) {
+        kf.quad(k, o);
+    } else {
+        const long long b = kf(k);
+        o[0] = b;
+        o[1] = b + ks;
+        o[2] = b + 2 * ks;
+        o[3] = b + 3 * ks;
+    }
+}
 
 // One operand's BK x BT slice (T = BM for A, BN for B) between global memory, registers and LDS,
 // moved by NT cooperating lanes (a workgroup, or one wavefront). `rs` = stride of the row/column
@@ -276,20 +295,20 @@ __device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][16 / W
 // offsets; 4 consecutive k are a_ks (b_ks) apart. The workgroup covers k in [kbeg, kbeg + K).
 template <int MODE, bool CHK>
 __device__ __forceinline__ void anvil_chunk_load_k(float (&r)[4], const float *__restrict__ p, long long toff,
-                                                   long long koff, long long ks, int t, int tmax, bool ok = true) {
+                                                   const long long (&ko)[4], int t, int tmax, bool ok = true) {
     if ((CHK && t >= tmax) || !ok) {
         r[0] = r[1] = r[2] = r[3] = 0.f;
         return;
     }
     if (MODE == ANVIL_LD_KC) {
-        const anvil_f32x4 v = *(const anvil_f32x4 *)(p + toff + koff);
+        const anvil_f32x4 v = *(const anvil_f32x4 *)(p + toff + ko[0]);
         r[0] = v.x;
         r[1] = v.y;
         r[2] = v.z;
         r[3] = v.w;
     } else {
 #pragma unroll
-        for (int s = 0; s < 4; s++) r[s] = p[toff + koff + (long long)s * ks];
+        for (int s = 0; s < 4; s++) r[s] = p[toff + ko[s]];
     }
 }
 
@@ -313,12 +332,14 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
 #define ANVIL_KP_LOAD(d, c)                                                                                \
     if (FULL || (c) < n) {                                                                                 \
         const int k_ = 8 * (c0 + (c)) + 4 * h;                                                             \
-        const long long ka_ = ak(k_), kb_ = bk(k_);                                                        \
+        long long ka_[4], kb_[4];                                                                          \
+        anvil_koffs<AMODE>(ak, k_, a_ks, ka_);                                                             \
+        anvil_koffs<BMODE>(bk, k_, b_ks, kb_);                                                             \
         _Pragma("unroll") for (int i = 0; i < TM; i++)                                                     \
-            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, ao[i], ka_, a_ks, m0 + 32 * i + r, M,            \
+            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, ao[i], ka_, m0 + 32 * i + r, M,                  \
                                             apred(m0 + 32 * i + r, k_));                                   \
         _Pragma("unroll") for (int j = 0; j < TN; j++)                                                     \
-            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, bo[j], kb_, b_ks, n0 + 32 * j + r, N,            \
+            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, bo[j], kb_, n0 + 32 * j + r, N,                  \
                                             bpred(n0 + 32 * j + r, k_));                                   \
     }
 #pragma unroll
