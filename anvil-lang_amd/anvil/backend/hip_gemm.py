@@ -624,6 +624,18 @@ class GemmPlan(Plan):
         sc.fwd, sc.canon = saved
         return "\n".join([f"    auto {name} = [=](float x) -> float {{"] + lines + [f"        return {v};", "    };"])
 
+    def tile_origin(self) -> str:
+        """m0, n0 of the workgroup's tile. A tall grid (tile rows ≥ 8 × tile columns: C4's 4096 x 256
+        products) takes the XCD-aware order: in launch order, linear id mod 8 would be the tile
+        column whenever the columns are a multiple of 8, so every XCD would read all of A (3-5 µs
+        of 35 measured). Square grids measured faster in launch order (C2's weight gradients)."""
+        if (os.environ.get("ANVIL_GEMM_SWIZZLE", "1") == "0" or self.tn * self.tm < 16
+                or self.tm < 8 * self.tn):
+            return f"    const int m0 = blockIdx.y * {self.BM}, n0 = blockIdx.x * {self.BN};"
+        return (f"    int tx_, ty_;\n"
+                f"    anvil_tile_of(blockIdx.y * {self.tn} + blockIdx.x, {self.tn}, {self.tm}, 8, tx_, ty_);\n"
+                f"    const int m0 = ty_ * {self.BM}, n0 = tx_ * {self.BN};")
+
     def k_table(self, which) -> str:
         """The file-scope table of an operand's k offsets (one int per k), when it has one."""
         tab = self.s.a_ktab if which == "a" else self.s.b_ktab
@@ -728,7 +740,7 @@ class GemmPlan(Plan):
         a_ptr = sc.buf(s.la.buf)
         b_ptr = sc.buf(s.lb.buf)
         body = [self.operand(sc, s.ea, s.la, "opa"), self.operand(sc, s.eb, s.lb, "opb"),
-                f"    const int m0 = blockIdx.y * {self.BM}, n0 = blockIdx.x * {self.BN};",
+                self.tile_origin(),
                 "    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;"]
         ca, cb = s.la.offset.coef, s.lb.offset.coef
         a_off = [str(s.la.offset.const)]

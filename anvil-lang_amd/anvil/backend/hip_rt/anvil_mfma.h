@@ -33,6 +33,20 @@ typedef float anvil_f32x4 __attribute__((ext_vector_type(4)));
 
 typedef int anvil_i32x4 __attribute__((ext_vector_type(4)));
 
+// XCD-aware tile order. Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
+// own L2: tile (tx, ty) of a tn x tm grid for linear id L is chosen so that the ids one XCD receives
+// (L mod 8 = x) cover one contiguous run p of tiles, and runs are walked in groups of G tile rows,
+// column by column: an XCD's tiles then share few row panels of A and column panels of B.
+__device__ __forceinline__ void anvil_tile_of(int L, int tn, int tm, int G, int &tx, int &ty) {
+    const int n = tn * tm, q = n / 8, rem = n % 8;
+    const int x = L % 8, r = L / 8;
+    const int p = x * q + min(x, rem) + r;
+    const int group = p / (G * tn), within = p % (G * tn);
+    const int gm = min(G, tm - group * G);
+    ty = group * G + within % gm;
+    tx = within / gm;
+}
+
 // The offsets of k .. k + 3 (k a multiple of 4) in an operand: kf(k) + s·ks, or four table entries.
 template <int MODE, class KF>
 __device__ __forceinline__ void anvil_koffs(KF kf, int k, long long ks, long long (&o)[4]) {

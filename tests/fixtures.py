@@ -27,9 +27,15 @@ def vectors(name):
     return np.load(os.path.join(GOLDEN, "vectors", f"{name}.npz"))
 
 
-def vector_names():
+# fixtures whose oracle run takes minutes (C2 whole: 500 full-size steps of the NumPy interpreter);
+# the oracle replays them only with ANVIL_SLOW_ORACLE=1, the GPU tests always compare against them
+SLOW = {"c2_full"}
+
+
+def vector_names(slow=False):
     d = os.path.join(GOLDEN, "vectors")
-    return sorted(f[:-4] for f in os.listdir(d) if f.endswith(".npz"))
+    names = sorted(f[:-4] for f in os.listdir(d) if f.endswith(".npz"))
+    return [n for n in names if slow or n not in SLOW]
 
 
 def stdout_of(z):

@@ -418,6 +418,12 @@ C2_KEEP = ["net.l1.W", "net.l1.b", "net.l2.W", "net.l2.b", "net.l3.W", "net.l3.b
 PROGRAMS = [
     # the workloads at the sizes BASELINE.json names (IR only: the interpreter would take hours)
     {"name": "c1_mlp", "source": C1},
+    # C1 and C2 whole, as BASELINE.json states them, through the reference interpreter: the printed
+    # loss and accuracy and the last layer's trained weights
+    {"name": "c1_full", "source": C1, "interp": True, "keep": ["net.l2.W", "net.l2.b"]},
+    {"name": "c2_full", "source": C2, "interp": True, "keep": ["net.l3.W", "net.l3.b"]},
+    {"name": "c2_full10", "source": C2, "consts": {"STEPS": 10}, "interp": True,
+     "keep": ["net.l1.b", "net.l2.b", "net.l3.W", "net.l3.b"]},
     {"name": "c2_wide_mlp", "source": C2},
     {"name": "c4_transformer", "source": C4},
     {"name": "c4_transformer_t256", "source": C4, "consts": {"T": 256}},
@@ -455,9 +461,9 @@ PROGRAMS = [
      "function": {"name": "norm", "args": [([48, 200], "f32"), ([200], "f32"), ([200], "f32")]}},
     {"name": "c3_linear_small", "source": C3_LINEAR, "interp": True,
      "function": {"name": "linear", "args": [([96, 80], "f32"), ([72, 80], "f32"), ([72], "f32")]}},
-    # a product of 1024 x 1024 outputs over K = 512: the pipelined K split with 1024 tiles
-    {"name": "c3_linear_w2", "source": C3_LINEAR, "interp": True,
-     "function": {"name": "linear", "args": [([1024, 512], "f32"), ([1024, 512], "f32"), ([1024], "f32")]}},
+    # a tall product (2048 x 128 outputs: 64 x 4 tiles), launched in the XCD-aware tile order
+    {"name": "c3_linear_tall", "source": C3_LINEAR, "interp": True,
+     "function": {"name": "linear", "args": [([2048, 64], "f32"), ([128, 64], "f32"), ([128], "f32")]}},
     {"name": "c3_attention_small", "source": C3_ATTENTION, "interp": True,
      "function": {"name": "attention", "args": [([2, 64, 32], "f32")] * 3}},
     # shapes the one-kernel attention takes (head size 64 and 128, keys a multiple of 128)

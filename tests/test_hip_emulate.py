@@ -16,7 +16,7 @@ from hiprun import function_call, kept_buffers, outputs_match, patched_program, 
 
 PROGRAMS = ["hello", "linreg", "attention_train", "split", "scatter", "integers", "formats", "control",
             "products", "c1_small", "c2_small", "c2_steps100", "mnist_like", "c4_small", "c4_mid", "c5_small", "c5_mid"]
-FUNCTIONS = ["c3_softmax_small", "c3_layernorm_small", "c3_linear_small", "c3_linear_w2", "c3_attention_small",
+FUNCTIONS = ["c3_softmax_small", "c3_layernorm_small", "c3_linear_small", "c3_linear_tall", "c3_attention_small",
              "c3_attention_d64", "c3_attention_d128"]
 TRAINED = {"c2_steps100", "c2_small", "c1_small", "mnist_like", "linreg", "attention_train", "c5_mid", "c4_mid"}
 

@@ -7,6 +7,7 @@ outputs). Closed forms: float64 NumPy restatements of softmax, layer norm, the l
 attention (prelude.anvil:28-43, pyapi.py test style), and the shuffle against brute force.
 """
 import io
+import os
 
 import numpy as np
 import pytest
@@ -15,7 +16,7 @@ from fixtures import load_ir, run_oracle, stdout_of, vector_names, vectors
 from oracle import interp
 
 
-@pytest.mark.parametrize("name", vector_names())
+@pytest.mark.parametrize("name", vector_names(slow=os.environ.get("ANVIL_SLOW_ORACLE") == "1"))
 def test_oracle_matches_reference_interpreter(name):
     prog, data = load_ir(name)
     z = vectors(name)
