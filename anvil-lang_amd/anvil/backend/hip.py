@@ -303,8 +303,11 @@ class HipGen:
             g = self.gemm.match(self, k, name)
             if g is not None:
                 if os.environ.get("ANVIL_GEMM_FUSE", "1") == "0" or self.check:   # no epilogue fusion
+                    g.settle()
                     return g, 1
-                return g, 1 + self.absorb_followers(g, stmts, i + 1)
+                used = 1 + self.absorb_followers(g, stmts, i + 1)
+                g.settle()
+                return g, used
         sl = HK.slice_count(k, self.emulate)
         if sl > 1:
             return HK.SlicePlan(self, k, name, sl), 1

@@ -507,8 +507,10 @@ class GemmPlan(Plan):
         if s.b_ktab:
             self.bmode = "ANVIL_LD_KT"
         self.slab = 0
-        # tuning: $ANVIL_GEMM_FORCE = comma-separated "tile64" | "tile128" | "ksplit:W:U" | "slab:KC",
-        # each optionally "@NN" / "@NT" / "@TN" (only products whose operands load that way)
+        self.ptm = self.ptn = 1             # 32 x 32 MFMA tiles per wavefront in the pipelined split
+        # tuning: $ANVIL_GEMM_FORCE = comma-separated "tile64" | "tile128" | "ksplit:W:U" | "slab:KC" |
+        # "kpipe:W:TM:TN", each optionally "@NN" / "@NT" / "@TN" (only products whose operands load
+        # that way)
         layout = {("ANVIL_LD_KC", "ANVIL_LD_RC"): "NN", ("ANVIL_LD_KC", "ANVIL_LD_KC"): "NT",
                   ("ANVIL_LD_RC", "ANVIL_LD_RC"): "TN"}.get((self.amode, self.bmode), "?")
         for force in os.environ.get("ANVIL_GEMM_FORCE", "").split(","):
@@ -522,18 +524,33 @@ class GemmPlan(Plan):
             elif parts[0] == "slab":
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.slab, self.waves = int(parts[1]), 4
+            elif parts[0] == "kpipe":
+                self.waves, self.ptm, self.ptn = int(parts[1]), int(parts[2]), int(parts[3])
+                self.sched, self.BM, self.BN = "ksplit", 32 * self.ptm, 32 * self.ptn
             else:
                 self.sched, self.BM, self.BN = "ksplit", 32, 32
                 self.waves, self.unroll = int(parts[1]), int(parts[2])
         if (s.a_gather or s.b_gather or s.k_multi or s.a_multi or s.b_multi or s.a_ktab or s.b_ktab
                 or min(s.M, s.N) < MIN_SIDE):                   # the pipelined K split only
-            self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
+            if self.ptm * self.ptn == 1:
+                self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
+            self.pipe = True
+        self.forced = any(f.partition("@")[0] for f in os.environ.get("ANVIL_GEMM_FORCE", "").split(","))
+        self.followers = []             # (kernel, var map, forwarded loads) run in the epilogue
+        self.layout()
+
+    def layout(self):
+        """What follows from the schedule: the K split across workgroups, pipeline depth, workgroup
+        size and tile grid."""
+        s = self.s
         self.pipe = self.pipe and self.sched == "ksplit" and not self.slab
+        if not self.pipe:
+            self.ptm = self.ptn = 1
         # K split across workgroups as well, when the output has few tiles and K is long (a
         # convolution's weight gradient: 64 x 288 outputs, K = 73728): each workgroup computes a
         # slice of K into a partial tile, and a second kernel adds the S partials in order and runs
         # the epilogue (see GemmReducePlan)
-        tiles = -(-s.M // 32) * -(-s.N // 32) * s.B
+        tiles = -(-s.M // self.BM) * -(-s.N // self.BN) * s.B if self.pipe else -(-s.M // 32) * -(-s.N // 32) * s.B
         self.kslices, self.kslice = 1, s.K
         if (self.pipe and tiles * self.waves < CU_WAVES // 2 and s.K >= 4096
                 and os.environ.get("ANVIL_GEMM_SPLITK", "1") != "0"):
@@ -545,7 +562,37 @@ class GemmPlan(Plan):
         self.threads = 64 * self.waves if self.sched == "ksplit" else 256
         self.tm = -(-s.M // self.BM)
         self.tn = -(-s.N // self.BN)
-        self.followers = []             # (kernel, var map, forwarded loads) run in the epilogue
+
+    def settle(self):
+        """Once the epilogue is known (its followers absorbed): a product whose epilogue is light (a
+        bias, a plain store) and whose operands load plainly takes the larger per-wavefront tiles; a
+        heavy epilogue (GELU, Adam: each lane of a one-wavefront workgroup would run it for 64
+        outputs, serially; C4's GELU products measured 17 µs slower) or per-element operand
+        addressing (a convolution's input through its table: 14 µs slower) keeps four wavefronts."""
+        from .hip_cost import expr_ops
+        s = self.s
+        light = not self.followers and sum(expr_ops(st.value) for st in self.k.stmts) <= 2
+        plain = not (s.a_gather or s.b_gather or s.k_multi or s.a_multi or s.b_multi or s.a_ktab or s.b_ktab)
+        if (light and plain and not self.forced and s.K % 8 == 0 and min(s.M, s.N) >= MIN_SIDE and not self.slab
+                and os.environ.get("ANVIL_GEMM_PIPE", "1") != "0"):
+            self.choose_pipe_tiles()
+            self.layout()
+
+    def choose_pipe_tiles(self):
+        """The pipelined K split's shape: W wavefronts per workgroup splitting K, each computing TM x TN
+        32 x 32 MFMA tiles. The largest tiles that still give every SIMD a wavefront (CU_WAVES of
+        them) win: the loaded operands serve TN (TM) products each and the wavefront carries
+        independent accumulator chains. Measured (fp32, one MI355X): 8192 x 4096 x 4096 at 139
+        TFLOP/s with one wavefront of 2 x 4 tiles (116 with the LDS-staged 128 x 128 tile); C4's
+        4096 x 1024 x 256 at 79-84 with 2 x 2 (68-73); 4096 x 256 x 1024 at 84 with four wavefronts
+        of 1 x 2 (77); batch-256 products stay at four wavefronts of one tile."""
+        s = self.s
+        for W, TM, TN, kmin in ((1, 2, 4, 0), (1, 2, 2, 0), (4, 1, 2, 512), (4, 1, 1, 0)):
+            if -(-s.M // (32 * TM)) * -(-s.N // (32 * TN)) * s.B * W >= CU_WAVES and s.K >= kmin:
+                break
+        self.sched, self.slab, self.pipe = "ksplit", 0, True
+        self.waves, self.ptm, self.ptn = W, TM, TN
+        self.BM, self.BN = 32 * TM, 32 * TN
 
     def hoistable(self, stages):
         """(stage, load) pairs of the epilogue that may be issued before the K loop: plain loads of
@@ -576,7 +623,7 @@ class GemmPlan(Plan):
             return 4 * (2 * 2 * self.slab * 33 + 4 * 16 * 64)
         if self.sched == "tile":
             return 2 * 4 * 16 * ((self.BM + 4) + (self.BN + 4))
-        return self.waves * 16 * 64 * 4
+        return self.waves * self.ptm * self.ptn * 16 * 64 * 4
 
     def absorb(self, e, how):
         m, fwd = how
@@ -775,14 +822,25 @@ class GemmPlan(Plan):
             value = "acc.c[ti][tj][vv]"
         else:
             W = self.waves
+            TM, TN = self.ptm, self.ptn
             per = 16 // W
-            loop = ["#pragma unroll", f"    for (int q = 0; q < {per}; q++) {{",
-                    f"        const int vv = {per} * wave + q;",
-                    "        const int mi = m0 + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
-                    "        const int ni = n0 + (lane & 31);",
-                    f"        if (mi >= {s.M} || ni >= {s.N}) continue;"]
-            slot = "q"
-            chk = lambda n: "true" if n % 32 else "false"
+            if TM * TN == 1:
+                loop = ["#pragma unroll", f"    for (int q = 0; q < {per}; q++) {{",
+                        f"        const int vv = {per} * wave + q;",
+                        "        const int mi = m0 + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
+                        "        const int ni = n0 + (lane & 31);",
+                        f"        if (mi >= {s.M} || ni >= {s.N}) continue;"]
+                slot = "q"
+            else:
+                loop = ["#pragma unroll", f"    for (int ijq = 0; ijq < {TM * TN * per}; ijq++) {{",
+                        f"        const int ti = ijq / {TN * per}, tj = (ijq / {per}) % {TN}, q = ijq % {per};",
+                        f"        const int vv = {per} * wave + q;",
+                        "        const int mi = m0 + 32 * ti + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
+                        "        const int ni = n0 + 32 * tj + (lane & 31);",
+                        f"        if (mi >= {s.M} || ni >= {s.N}) continue;"]
+                slot = "ijq"
+                per = TM * TN * per
+            chk = lambda n, t=32: "true" if n % t else "false"
             if self.slab:
                 kargs = (f"pa, {s.a_rs}LL, {s.a_ks}LL, pb, {s.b_rs}LL, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, {s.K}, "
                          "opa, opb")
@@ -802,13 +860,13 @@ class GemmPlan(Plan):
                 kargs = (f"pa, arow, ak, {a_ks}LL, pb, brow, bk, {b_ks}LL, {s.M}, {s.N}, m0, n0, {krange}, "
                          "opa, opb")
                 nch = -(-(self.kslice // 8) // W)
-                main = [f"    float part[1][1][{per}];",
-                        f"    anvil_mm_tile_kpipe<{W}, 1, 1, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
-                        f"{chk(s.M)}, {chk(s.N)}>(part, {kargs});"]
+                main = [f"    float part[{TM}][{TN}][{16 // W}];",
+                        f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
+                        f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}>(part, {kargs});"]
             else:
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]
-            value = "part[0][0][q]"
+            value = "part[0][0][q]" if TM * TN == 1 else "part[ti][tj][q]"
         def head():                                   # after the body: its buffers are the parameters
             return [self.k_table("a") + self.k_table("b") + self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
                     + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, B {self.bmode[9:]}"

@@ -87,6 +87,12 @@ fn linear(x: [n, k], W: [o, k], b: [o]):
     return y
 """
 
+C3_BMM = """
+fn bmm(a: [b, m, k], w: [b, k, n]):
+    y[t, i, j] = sum a[t, i, c] * w[t, c, j]
+    return y
+"""
+
 C3_ATTENTION = """
 fn attention(q: [b, t, d], k: [b, t, d], v: [b, t, d]):
     s[n, i, j] = sum q[n, i, c] * k[n, j, c] / sqrt(d)
@@ -434,6 +440,12 @@ PROGRAMS = [
      "function": {"name": "norm", "args": [([8192, 1024], "f32"), ([1024], "f32"), ([1024], "f32")]}},
     {"name": "c3_linear", "source": C3_LINEAR,
      "function": {"name": "linear", "args": [([8192, 4096], "f32"), ([4096, 4096], "f32"), ([4096], "f32")]}},
+    # products whose shapes take one wavefront of 2 x 2 MFMA tiles (IR only; the GPU tests check them
+    # against float64 closed forms)
+    {"name": "c3_linear_mid", "source": C3_LINEAR,
+     "function": {"name": "linear", "args": [([4096, 256], "f32"), ([1024, 256], "f32"), ([1024], "f32")]}},
+    {"name": "c3_bmm", "source": C3_BMM,
+     "function": {"name": "bmm", "args": [([64, 256, 64], "f32"), ([64, 64, 256], "f32")]}},
     {"name": "c3_attention", "source": C3_ATTENTION,
      "function": {"name": "attention", "args": [([4, 2048, 128], "f32")] * 3}},
     # the same workloads at sizes the interpreter finishes in seconds (IR + vectors)

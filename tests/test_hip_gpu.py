@@ -137,6 +137,32 @@ def test_gpu_linear_at_full_size_matches_closed_form():
     np.testing.assert_allclose(got[rows], want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
 
 
+def test_gpu_linear_2x2_tiles_matches_closed_form():
+    """A linear layer of C4's MLP shape, [4096, 256] × [1024, 256]ᵀ, which takes one wavefront of
+    2 x 2 MFMA tiles per workgroup: one row of each 64-row tile against float64 NumPy."""
+    print("gpu linear 4096x1024x256", flush=True)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4096, 256)).astype(np.float32)
+    w = rng.standard_normal((1024, 256)).astype(np.float32)
+    b = rng.standard_normal(1024).astype(np.float32)
+    got = _full_size_call("c3_linear_mid", [x, w, b])
+    rows = 64 * np.arange(64) + (29 * np.arange(64)) % 64
+    want = x[rows].astype(np.float64) @ w.astype(np.float64).T + b
+    np.testing.assert_allclose(got[rows], want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
+
+
+def test_gpu_batched_2x2_tiles_matches_closed_form():
+    """A batched product of C4's attention shape, 64 × ([256, 64] · [64, 256]), in 2 x 2 MFMA tiles
+    per wavefront with the batch in the grid: every batch's outputs against float64 NumPy."""
+    print("gpu bmm 64 x 256x256x64", flush=True)
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((64, 256, 64)).astype(np.float32)
+    w = rng.standard_normal((64, 64, 256)).astype(np.float32)
+    got = _full_size_call("c3_bmm", [a, w])
+    want = np.matmul(a.astype(np.float64), w.astype(np.float64))
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
+
+
 def _source_lines(prog, data):
     from anvil.backend import hip
     return hip.generate(prog, seed=data.get("seed", 0), library=True).splitlines()
