@@ -410,12 +410,19 @@ class DgradPlan(Plan):
         self.ops, self.rows, self.korder, self.side_pred = ops, rows, korder, side_pred
         self.tvars, self.sst, self.M, self.N, self.K = tvars, sst, M, N, K
         self.skip_stores = {(k.id, 0) for k in kernels if k is not S}     # dP is never written; dX once
-        self.tm, self.tn = -(-M // 32), -(-N // 32)
-        nch = -(-(K // 8) // 4)
+        # W wavefronts splitting K, each with TM x TN 32 x 32 tiles ($ANVIL_DGRAD_TILES = "W:TM:TN"):
+        # four with 1 x 2 measured best on C5 (50.8 µs; 1 x 1: 63.8, 1 x 4: 55.7, two waves of 1 x 2:
+        # 58.5), each weight load serving two tiles of positions
+        W, TM, TN = (int(x) for x in os.environ.get("ANVIL_DGRAD_TILES", "4:1:2").split(":"))
+        if M < 32 * TM or N < 32 * TN:
+            W, TM, TN = 4, 1, 1
+        self.W, self.TM, self.TN = W, TM, TN
+        self.tm, self.tn = -(-M // (32 * TM)), -(-N // (32 * TN))
+        nch = -(-(K // 8) // W)
         self.nch, self.depth = nch, min(2 if nch <= 32 else 4, nch)
 
     def grid(self):
-        return (self.tn, self.tm, 1), 256
+        return (self.tn, self.tm, 1), 64 * self.W
 
     def source(self) -> str:
         from . import hip_gemm
@@ -426,7 +433,8 @@ class DgradPlan(Plan):
         for n in (0, 1):
             e, ld, off1, off2 = self.ops[n]
             body.append(hip_gemm.GemmPlan.operand(self, sc, e, ld, f"op{names[n]}"))
-        body += ["    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;"]
+        W, TM, TN = self.W, self.TM, self.TN
+        body += [f"    const int m0 = blockIdx.y * {32 * TM}, n0 = blockIdx.x * {32 * TN};"]
         for n in (0, 1):
             e, ld, off1, off2 = self.ops[n]
             body.append(f"    const float *p{names[n]} = {sc.buf(ld.buf)} + ({off2.const}LL);")
@@ -446,17 +454,19 @@ class DgradPlan(Plan):
                 body.append(f"    anvil_all_pred {names[n]}pred;")
         inner = self.korder[-1]
         a_ks, b_ks = self.ops[0][3].coef(inner), self.ops[1][3].coef(inner)
-        chk = lambda x: "true" if x % 32 else "false"
-        body += ["    float part[1][1][4];",
-                 f"    anvil_mm_tile_kpipe<4, 1, 1, ANVIL_LD_ANY, ANVIL_LD_ANY, {self.nch}, {self.depth}, {chk(self.M)}, "
-                 f"{chk(self.N)}>(part, pa, arow, ak, {a_ks}LL, pb, brow, bk, {b_ks}LL, {self.M}, {self.N}, m0, n0, "
-                 f"0, {self.K}, opa, opb, apred, bpred);",
+        chk = lambda x, t: "true" if x % t else "false"
+        per = 16 // W
+        body += [f"    float part[{TM}][{TN}][{per}];",
+                 f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, ANVIL_LD_ANY, ANVIL_LD_ANY, {self.nch}, {self.depth}, "
+                 f"{chk(self.M, 32 * TM)}, {chk(self.N, 32 * TN)}>(part, pa, arow, ak, {a_ks}LL, pb, brow, bk, "
+                 f"{b_ks}LL, {self.M}, {self.N}, m0, n0, 0, {self.K}, opa, opb, apred, bpred);",
                  "    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;",
                  "#pragma unroll",
-                 "    for (int q = 0; q < 4; q++) {",
-                 "        const int vv = 4 * wave + q;",
-                 "        const int mi = m0 + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
-                 "        const int ni = n0 + (lane & 31);",
+                 f"    for (int ijq = 0; ijq < {TM * TN * per}; ijq++) {{",
+                 f"        const int ti = ijq / {TN * per}, tj = (ijq / {per}) % {TN}, q = ijq % {per};",
+                 f"        const int vv = {per} * wave + q;",
+                 "        const int mi = m0 + 32 * ti + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
+                 "        const int ni = n0 + 32 * tj + (lane & 31);",
                  f"        if (mi >= {self.M} || ni >= {self.N}) continue;"]
         dm, dn = _digits(self.rows[0], "mi"), _digits(self.rows[1], "ni")
         out = [str(self.sst.offset.const)] if self.sst.offset.const else []
@@ -465,9 +475,9 @@ class DgradPlan(Plan):
             out.append(f"{c}LL * (long long){d}")
         target = f"{sc.buf(self.sst.buf)}[{' + '.join(out)}]"
         base = "0.0f" if self.zeroed else target
-        body.append(f"        {target} = {base} + {flit(self.alpha)} * part[0][0][q];")
+        body.append(f"        {target} = {base} + {flit(self.alpha)} * part[ti][tj][q];")
         body.append("    }")
         head = [f"// conv-dgrad: {self.G.name} (product into an im2col-shaped gradient) and {self.S.name} (its "
                 f"scatter) as one product · {self.M}x{self.N}x{self.K}, window terms over the edge skipped",
-                self.header(256)]
+                self.header(64 * W)]
         return "\n".join(head + body + ["}"])
