@@ -1,0 +1,86 @@
+"""The HIP generator's IR rewrites keep each program's meaning: the oracle (oracle/interp.py, pinned
+to the reference interpreter by test_oracle.py) runs the program before and after each rewrite and
+must print and store the same thing. The rewrites only move or re-address work, so integers and the
+printed text are identical; floats are identical where the sums keep their order and within 1e-5
+where a rewrite splits one summed variable into several (NumPy then sums over more axes).
+"""
+import numpy as np
+
+from fixtures import load_ir, run_oracle
+from hiprun import kept_buffers, outputs_match, tensors_match
+
+from anvil import ir
+from anvil.backend import hip_analysis as A
+from anvil.backend import hip_conv, hip_gemm
+
+
+def kernels(prog):
+    return [st.kernel for blk in ir.walk_blocks(prog.main) for st in blk.stmts if isinstance(st, ir.KernelStmt)]
+
+
+def run(prog, data, keep):
+    m, out = run_oracle(prog, data)
+    by_name = {b.name: b for b in prog.buffers}
+    return out, {k: m.arr(by_name[k])[:by_name[k].numel].reshape(by_name[k].shape).copy() for k in keep}
+
+
+def test_implicit_convolution_rewrite_keeps_the_program():
+    """c5_mid: both products over the second convolution's im2col copy read the copy's source
+    through the window (their merged variables split back out), and the copy is dropped."""
+    prog, data = load_ir("c5_mid")
+    new = hip_conv.forward_im2col_copies(prog)
+    before, after = kernels(prog), kernels(new)
+    assert len(after) == len(before) - 1                          # the im2col copy of conv2 is gone
+    split = [k for k in after if k not in before and k.red is not None]
+    assert len(split) == 2 and all(len(k.domain) + len(k.red.vars) > 4 for k in split)
+    keep = kept_buffers("c5_mid")
+    out0, bufs0 = run(prog, data, keep)
+    out1, bufs1 = run(new, data, keep)
+    assert outputs_match(out0, out1, rtol=1e-5) is None
+    for k in keep:
+        assert tensors_match(bufs0[k], bufs1[k], rtol=1e-5) is None, k
+
+
+def test_gathered_batch_rows_keep_the_program():
+    """c2_small: the first product reads X[perm[s·B + i], ·] instead of the gathered batch copy;
+    the same values, summed in the same order."""
+    prog, data = load_ir("c2_small")
+    new = hip_gemm.forward_gather_copies(prog, A.host_scalars(prog))
+
+    def gathered_products(p):
+        return [k for k in kernels(p) if k.red is not None and k.red.op == "sum"
+                and any(ld.offset.gathers() for ld in ir.loads_in(k.red.body))]
+    assert len(gathered_products(new)) == len(gathered_products(prog)) + 1
+    keep = kept_buffers("c2_small")
+    out0, bufs0 = run(prog, data, keep)
+    out1, bufs1 = run(new, data, keep)
+    assert out0 == out1
+    for k in keep:
+        np.testing.assert_array_equal(bufs0[k], bufs1[k], err_msg=k)
+
+
+def test_sunk_scalar_kernels_keep_the_program():
+    """c2_small: the loss (a one-value reduction) moves past the kernels it commutes with."""
+    prog, data = load_ir("c2_small")
+    new = A.sink_scalar_kernels(prog)
+    assert [k.id for k in kernels(new)] != [k.id for k in kernels(prog)]
+    keep = kept_buffers("c2_small")
+    out0, bufs0 = run(prog, data, keep)
+    out1, bufs1 = run(new, data, keep)
+    assert out0 == out1
+    for k in keep:
+        np.testing.assert_array_equal(bufs0[k], bufs1[k], err_msg=k)
+
+
+def test_split_vars_is_the_row_major_index():
+    """A variable t of extent 12 split into (a, b) of extents (3, 4): every offset 5·t becomes
+    20·a + 5·b, in the domain's place of t."""
+    t, i = ir.Var("t", 12), ir.Var("i", 7)
+    buf = ir.Buffer("x", (7, 12), "f32", "temp")
+    k = ir.Kernel([i, t], [ir.Store(buf, ir.Affine(0, {i: 12, t: 1}), ir.Load(buf, ir.Affine(3, {t: 5})))])
+    a, b = ir.Var("a", 3), ir.Var("b", 4)
+    k2 = hip_conv.split_vars(k, {t: [a, b]})
+    assert k2.domain == [i, a, b]
+    st = k2.stmts[0]
+    assert st.offset == ir.Affine(0, {i: 12, a: 4, b: 1})
+    assert st.value.offset == ir.Affine(3, {a: 20, b: 5})
