@@ -13,7 +13,8 @@ and after. `value` is samples/s over those K steps.
 
 The roofline object is for the generated kernel that takes the most device time in a second,
 profiled run of the same program (HIP events around every launch on the library's stream):
-achieved = its algorithmic FLOPs (or bytes) per launch / its mean launch time.
+achieved = its algorithmic FLOPs (or bytes) per launch / its mean launch time. step_roofline puts
+the whole step beside its serial roofline: every launch of a step at its own bound, summed.
 
 cpu_baseline: this repository's NumPy interpreter of the same IR (oracle/interp.py, which follows
 the reference interpreter anvil/interp.py) timed on this host for a few full-size steps.
@@ -128,6 +129,18 @@ def roofline(prof, library: str):
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "frac": round(achieved / (PEAK_HBM / 1e9), 4), "traffic": traffic, "kernel": label,
             "mean_us": round(t * 1e6, 3), "bytes_per_launch": nbytes}
+
+
+def step_roofline(prof, ms_per_step: float):
+    """The whole step against its serial roofline: each launch of a step at its own bound (its
+    FLOPs at the fp32 MFMA peak or its bytes at the HBM peak, whichever takes longer), summed, over
+    the measured step time."""
+    t = 0.0
+    for label, ms, calls, flops, nbytes in prof:
+        if calls >= STEPS_IN_PROGRAM:
+            t += calls / STEPS_IN_PROGRAM * max(flops / PEAK_FP32_MFMA, nbytes / PEAK_HBM)
+    return {"t_roofline_us": round(t * 1e6, 2), "t_step_us": round(ms_per_step * 1e3, 2),
+            "frac": round(t * 1e3 / ms_per_step, 4)}
 
 
 COPY_ELEMS = 1 << 24          # the calibration copy: 64 MiB read, 64 MiB written per launch
@@ -291,6 +304,7 @@ def main() -> int:
                    "graph_replay": args.graphs,
                    "program_wall_s": round(wall, 3)},
         "roofline": roofline(prof, os.path.basename(lib.path)),
+        "step_roofline": step_roofline(prof, ms / args.steps),
     }
     if not args.no_cpu:
         cpu = cpu_baseline(prog, data, args.cpu_steps)

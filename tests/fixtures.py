@@ -27,9 +27,10 @@ def vectors(name):
     return np.load(os.path.join(GOLDEN, "vectors", f"{name}.npz"))
 
 
-# fixtures whose oracle run takes minutes (C2 whole: 500 full-size steps of the NumPy interpreter);
-# the oracle replays them only with ANVIL_SLOW_ORACLE=1, the GPU tests always compare against them
-SLOW = {"c2_full"}
+# fixtures whose oracle run takes minutes (C2 whole: 500 full-size steps of the NumPy interpreter;
+# C5 at full size: its im2col products broadcast over 10^9 elements a step); the oracle replays them
+# only with ANVIL_SLOW_ORACLE=1, the GPU tests always compare against them
+SLOW = {"c2_full", "c5_full3"}
 
 
 def vector_names(slow=False):

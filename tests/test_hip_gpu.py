@@ -30,9 +30,15 @@ def test_gpu_program_matches_reference(name):
         assert problem is None, f"{k}: {problem}"
 
 
-@pytest.mark.parametrize("name", ["c1_full", "c2_full", "c2_full10"])
+@pytest.mark.parametrize("name", ["c1_full", "c2_full", "c2_full10", "c5_full3"])
 def test_gpu_full_size_program_matches_reference(name):
-    """C1 and C2 exactly as BASELINE.json states them, against the reference interpreter's own runs.
+    """C1, C2 and C5 as BASELINE.json states them, against the reference interpreter's own runs
+    (C5 for 3 of its 300 steps: the loss and the trained weights, through the implicit-GEMM
+    convolutions, the fused input gradient and the sliced bias gradients; its first steps raise the
+    loss from 2.3 to 5.7, and a ReLU or max-pool choice that flips between two nearly equal values
+    sends a whole gradient elsewhere, so a different summation order shows up in a few weights:
+    the loss must agree to 1e-3, 99 % of every tensor to 0.5 % of its largest value and all of it
+    to 2 %; measured 0.09 %, and 0.12 % / 0.9 % at the worst tensor).
     C1 (784-128-10 MLP, SGD, batch 64, one epoch and the test accuracy): the printed loss and
     accuracy and the last layer's trained weights. C2 (784-1024-1024-10 MLP, Adam, batch 256, 500
     steps over 65,536 samples): the printed loss. C2 for 10 steps at full size: the printed loss and
@@ -53,7 +59,11 @@ def test_gpu_full_size_program_matches_reference(name):
     assert problem is None, problem
     for k in keep:
         ref, got = z[f"buf:{k}"].astype(np.float64), arrays[k].astype(np.float64)
-        if name == "c2_full10":
+        if name == "c5_full3":
+            err = np.abs(got - ref) / np.abs(ref).max()
+            assert err.max() <= 0.02, f"{k}: max |error| {err.max():.3g} of the largest value"
+            assert np.percentile(err, 99) <= 0.005, f"{k}: 99th percentile {np.percentile(err, 99):.3g}"
+        elif name == "c2_full10":
             moved = 1e-3 * 10                              # lr · steps
             err = np.abs(got - ref) / moved
             assert err.max() <= 0.05, f"{k}: max |error| {err.max():.3g} of lr·steps"
