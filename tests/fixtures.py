@@ -30,7 +30,7 @@ def vectors(name):
 # fixtures whose oracle run takes minutes (C2 whole: 500 full-size steps of the NumPy interpreter;
 # C5 at full size: its im2col products broadcast over 10^9 elements a step); the oracle replays them
 # only with ANVIL_SLOW_ORACLE=1, the GPU tests always compare against them
-SLOW = {"c2_full", "c5_full3"}
+SLOW = {"c2_full", "c5_full3", "c4_full2"}
 
 
 def vector_names(slow=False):

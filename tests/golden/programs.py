@@ -428,6 +428,8 @@ PROGRAMS = [
     # loss and accuracy and the last layer's trained weights
     {"name": "c1_full", "source": C1, "interp": True, "keep": ["net.l2.W", "net.l2.b"]},
     {"name": "c2_full", "source": C2, "interp": True, "keep": ["net.l3.W", "net.l3.b"]},
+    {"name": "c4_full2", "source": C4, "consts": {"STEPS": 2}, "interp": True,
+     "keep": ["net.blocks.0.Wq", "net.blocks.3.up.W", "net.out.W", "net.out.b"]},
     {"name": "c5_full3", "source": C5, "consts": {"STEPS": 3}, "interp": True,
      "keep": ["net.c1.W", "net.c1.b", "net.c2.W", "net.c2.b", "net.fc2.W"]},
     {"name": "c2_full10", "source": C2, "consts": {"STEPS": 10}, "interp": True,
