@@ -314,9 +314,9 @@ def match_dgrad(gen, stmts: list, i: int):
     scat = scatter_targets(S)
     if scat is None or dX.id in {b.id for b in A.kernel_reads(G)}:
         return None
-    if zero is not None and not _zero_fill(zero, dX):
-        return None
     targets, summed = scat
+    if zero is not None and (not _zero_fill(zero, dX) or ir.prod(t[1] for t in targets) != dX.numel):
+        return None                                   # the fill is absorbed only if every element is a target
     # dP's element as S reads it, in G's variables: each of G's (merged) variables is a mixed-radix
     # number over S's variables
     loff = sst.value.offset

@@ -9,7 +9,7 @@ import sys
 
 import pytest
 
-from fixtures import ROOT, ROOT_PKG, load_ir
+from fixtures import ROOT, load_ir
 
 
 def declared_functions():

@@ -11,7 +11,7 @@ import os
 import numpy as np
 import pytest
 
-from fixtures import load_ir, stdout_of, vectors
+from fixtures import stdout_of, vectors
 from hiprun import function_call, kept_buffers, outputs_match, patched_program, run_program, tensors_match
 
 PROGRAMS = ["hello", "linreg", "attention_train", "split", "scatter", "integers", "formats", "control",
