@@ -110,6 +110,9 @@ class Scope:
         """A register already holding this load's value, or None."""
         return None
 
+    def loaded(self, ld: Load, name: str) -> None:
+        """Called once a load's value is held in the C constant `name`."""
+
     def int_offsets(self, b: ir.Buffer) -> bool:
         """May offsets into b be computed in 32-bit arithmetic?"""
         return b.root.numel < (1 << 30)
@@ -198,6 +201,8 @@ class Emitter:
         name = self.tmp()
         self.emit(f"const {ctype(e.dtype)} {name} = {text};")
         self.memo[key] = name
+        if isinstance(e, Load):
+            self.s.loaded(e, name)
         return name
 
     def as_float(self, e) -> str:

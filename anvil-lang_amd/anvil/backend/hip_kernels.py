@@ -965,18 +965,120 @@ class RowBlockBuilder:
 
 
 class RowBlockScope(KernelScope):
-    """Loads of the chain's own row slices kept in LDS read the LDS copy."""
+    """Loads of the chain's own row slices kept in LDS read the LDS copy; operands the plan keeps
+    in registers (hoisted per-row loads, values forwarded from an earlier stage) read those."""
 
     def __init__(self, plan):
         super().__init__(plan)
         self.em = None
+        self.part = "stmts"             # which part of the stage is being emitted: "body" / "stmts"
+        self.q = None                   # a block stage's output being accumulated (its body)
+        self.red_index = "0"            # a serial stage's flat reduction index (its body)
+        self.hoisted: dict = {}         # load key -> register
+        self.targets: dict = {}         # (part, load key) -> (slot, map from the index to the slot's)
+        self.sources: dict = {}         # (part, load key) -> slot
+
+    def inner(self) -> str:
+        """The index of the current load among the part's I (see RowBlockPlan.addresses)."""
+        if self.part != "body":
+            return "0"
+        return self.red_index if self.q is None else str(self.q)
 
     def override_load(self, ld):
         b = ld.buf.root
         if b.id in self.plan.shadow and self.em is not None:
             S = self.plan.shadow[b.id]
             return f"sh{b.id}[{self.em.affine(ld.offset, ld.buf)} - (int)row * {S}]"
+        key = ld.key()
+        if key in self.hoisted and self.part == "stmts":
+            return self.hoisted[key]
+        got = self.targets.get((self.part, key))
+        if got is not None:
+            slot, qmap = got
+            if len(set(qmap)) == 1:
+                q = str(qmap[0])
+            elif qmap == list(range(len(qmap))):
+                q = self.red_index
+            else:
+                q = f"fwq{slot}_{len(self.plan.qtables)}[{self.red_index}]"
+                self.plan.qtables.append((q.split("[")[0], qmap))
+            return f"fw{slot}[it_][{q}]"
         return super().override_load(ld)
+
+    def loaded(self, ld, name):
+        slot = self.sources.get((self.part, ld.key()))
+        if slot is not None and self.em is not None:
+            self.em.emit(f"fw{slot}[it_][{self.inner()}] = {name};")
+
+
+class RowStage:
+    """How RowBlockPlan.source() runs one kernel of the chain: "block" (every lane accumulates a
+    share of the reduction for all E outputs of the row, the shares then combined), "wave" (a
+    wavefront per output), "serial" (a lane per output, its reduction in the lane) or "map". The
+    lanes walk their index (the reduction's for "block", the outputs' otherwise: N of them) in
+    steps of T, `trips` times; a block stage's outputs are finished by lanes 0 .. E-1 (its tail)."""
+
+    def __init__(self, k, R: int, T: int):
+        self.k = k
+        self.E = ir.prod(v.extent for v in k.domain) // R
+        red = k.red
+        self.n = ir.prod(v.extent for v in red.vars) if red is not None else 1
+        if red is not None and red.op in RED_CODE and self.E <= 16 and self.n >= 256:
+            self.form = "block"
+        elif red is not None and red.op in RED_CODE and self.E < 64 and self.n > 64:
+            self.form = "wave"
+        else:
+            self.form = "serial" if red is not None else "map"
+        self.N = self.n if self.form == "block" else self.E
+        self.trips = -(-self.N // T)
+        self.split = _row_lane_rules(k.domain, self.E)
+        self.itform = False             # the lane loop counts its trips (it_), for forwarding
+
+    def parts(self) -> dict:
+        """Each part's loads (with the gathers' index loads): the body is the reduction's
+        expression (a block stage's lanes evaluate it for each of the E outputs, a serial stage's
+        lane for each reduction element), the statements run once per output."""
+        body, stmts = [], []
+        if self.k.red is not None:
+            _loads_of(self.k.red.body, body)
+        for st in self.k.stmts:
+            _loads_of(st.value, stmts)
+            if isinstance(st, ir.Store):
+                A.offset_loads(st.offset, stmts)
+        return {"body": body, "stmts": stmts}
+
+
+def _loads_of(e, out: list) -> None:
+    for x in ir.iter_expr(e):
+        if isinstance(x, Load):
+            out.append(x)
+            A.offset_loads(x.offset, out)
+        elif isinstance(x, ir.Index):
+            A.offset_loads(x.affine, out)
+
+
+def _row_lane_rules(vars_, E: int):
+    """How each variable decoded from row·E + e (e < E) splits into a part that depends on the row
+    and one that depends on e: (row divisor, row modulus, row scale, e divisor, e modulus), the
+    value being (row // rd) % rm · rs + (e // ed) % em; None if some variable mixes the two."""
+    out = []
+    for v, P in zip(vars_, ir.row_major_strides([v.extent for v in vars_])):
+        X = v.extent
+        if P % E == 0:                              # counts rows only
+            out.append((P // E, X, 1, 1, 1))
+        elif E % P == 0 and (X * P) % E == 0:        # rows (mod X·P/E) above, e // P below
+            out.append((1, X * P // E, E // P, P, E // P))
+        elif E % P == 0 and E % (X * P) == 0:        # within a row only
+            out.append((1, 1, 0, P, X))
+        else:
+            return None
+    return out
+
+
+def _digits(flat, vars_):
+    """Row-major digits of the flattened index (a NumPy array) over vars_."""
+    strides = ir.row_major_strides([v.extent for v in vars_])
+    return [(flat // s) % v.extent for v, s in zip(vars_, strides)]
 
 
 class RowBlockPlan(Plan):
@@ -987,10 +1089,18 @@ class RowBlockPlan(Plan):
     then combined by shuffles and LDS in a fixed order. Each buffer the chain writes is written in
     the row's own slice; a slice of up to SHADOW elements is also kept in LDS, where later stages
     read it (and a buffer no kernel outside the chain reads is not written to memory at all). A
-    barrier separates the stages."""
+    barrier separates the stages.
+
+    Operands that no stage writes are loaded once where they can be: a load that a later stage
+    repeats in the same lane and trip (C2's logits stage reads h2 and W3 for the row, and the
+    input-gradient stages after the softmax read the same h2 and W3 elements again) is forwarded
+    in registers (FORWARD_REGS per lane at most), and the loads of one-trip stages (a bias, the
+    row's label) are issued before the first stage instead of after the stages before them."""
 
     kind = "rowblock"
     SHADOW = 2048                   # elements of a row slice kept in LDS
+    FORWARD_REGS = 64               # registers per lane holding operands forwarded between stages
+    HOIST = 8                       # per-row operand loads issued before the first stage
 
     def __init__(self, gen, kernels, name, R: int):
         super().__init__(gen, kernels, name)
@@ -1019,6 +1129,126 @@ class RowBlockPlan(Plan):
                 total += S
                 if dead:
                     self.dead.add(b.id)
+        self.stages = [RowStage(k, R, self.threads) for k in kernels]
+        self.qtables: list = []
+        self.plan_reuse()
+
+    # ------------------------------------------------------------------ operand reuse
+    def reusable(self, st: RowStage, ld, part: str) -> bool:
+        """A load the analysis may move: of memory no stage writes, at an affine offset of the
+        stage's own variables."""
+        b = ld.buf.root
+        if not b.shape or b.id in self.chain_writes or b.id in self.shadow:
+            return False
+        ok = set(st.k.domain) | (set(st.k.red.vars) if part == "body" and st.k.red is not None else set())
+        return all(isinstance(t, Var) and t in ok for t in ld.offset.terms)
+
+    def addresses(self, st: RowStage, ld, part: str):
+        """The element each lane loads, split as row part (R,) + lane part (T, trips, I) (I: the
+        block stage's outputs, or the serial stage's reduction elements, for the body), with the
+        lanes that run the part (T, trips)."""
+        import numpy as np
+        T, R, k = self.threads, self.R, st.k
+        coef = ld.offset.terms
+        rows = np.arange(R, dtype=np.int64)
+        row = np.full(R, ld.offset.const, dtype=np.int64)
+        idx = np.arange(T, dtype=np.int64)[:, None] + T * np.arange(st.trips, dtype=np.int64)[None, :]
+        act = idx < st.N
+        x = np.zeros(idx.shape + (1,), dtype=np.int64)
+        # the domain's variables: e is the output q (a block stage's body) or the lane's index
+        e = np.arange(st.E, dtype=np.int64)[None, None, :] if st.form == "block" else idx[:, :, None]
+        for v, (rd, rm, rs, ed, em) in zip(k.domain, st.split):
+            c = coef.get(v, 0)
+            if c:
+                row = row + c * rs * ((rows // rd) % rm)
+                x = x + c * ((e // ed) % em)
+        if st.form == "block":                      # the body: reduction index idx
+            for v, d in zip(k.red.vars, _digits(idx, k.red.vars)):
+                x = x + coef.get(v, 0) * d[:, :, None]
+        else:
+            if part == "body":
+                r = np.arange(st.n, dtype=np.int64)
+                for v, d in zip(k.red.vars, _digits(r, k.red.vars)):
+                    x = x + coef.get(v, 0) * d[None, None, :]
+        return row, x, act
+
+    def plan_reuse(self) -> None:
+        """Choose the forwarded and the hoisted loads (see the class docstring)."""
+        import numpy as np
+        self.chain_writes = {b.id for k in self.kernels for b in A.kernel_writes(k)}
+        T = self.threads
+        self.slots: list = []                       # (C type, trips, I) of each forwarding array
+        used: dict = {}                             # slot -> {(trip, index)} that later stages read
+        cand: list = []                             # loads a later stage may take from registers
+        for st in self.stages:
+            st.targets, st.sources, st.hoisted = {}, {}, {}
+        for si, st in enumerate(self.stages):
+            if st.form == "wave" or st.split is None or st.trips > 8:
+                continue
+            mine = []
+            for part, loads in st.parts().items():
+                if st.form == "block" and part == "stmts":
+                    continue                        # the tail: lanes 0 .. E-1 once (hoisted below)
+                I = st.E if st.form == "block" else (st.n if part == "body" else 1)
+                if I > 16:
+                    continue
+                seen = set()
+                for ld in loads:
+                    key = ld.key()
+                    if key in seen or not self.reusable(st, ld, part):
+                        continue
+                    seen.add(key)
+                    row, x, act = self.addresses(st, ld, part)
+                    x = np.broadcast_to(x, (T, st.trips, I))
+                    match = None
+                    for c in cand:
+                        if c["buf"] is not ld.buf.root or c["stage"].trips < st.trips:
+                            continue
+                        d = c["row"] - row
+                        if not (d == d[0]).all() or not (c["act"][:, :st.trips] | ~act).all():
+                            continue
+                        xs = c["x"][:, :st.trips, :] + d[0]
+                        qmap = []
+                        for r in range(I):
+                            ok = ((xs == x[:, :, r][:, :, None]) | ~act[:, :, None]).all(axis=(0, 1))
+                            if not ok.any():
+                                break
+                            qmap.append(int(np.argmax(ok)))
+                        if len(qmap) == I:
+                            match = (c, qmap)
+                            break
+                    if match is None:
+                        mine.append({"stage": st, "part": part, "key": key, "buf": ld.buf.root, "dtype": ld.dtype,
+                                     "row": row, "x": x, "act": act, "slot": None})
+                        continue
+                    c, qmap = match
+                    need = {(t, q) for t in range(st.trips) for q in qmap}
+                    slot = c["slot"]
+                    extra = need - used.get(slot, set())
+                    if sum(len(u) for u in used.values()) + len(extra) > self.FORWARD_REGS:
+                        continue
+                    if slot is None:
+                        slot = c["slot"] = len(self.slots)
+                        self.slots.append((ctype(c["dtype"]), c["stage"].trips, c["x"].shape[2]))
+                        c["stage"].sources[(c["part"], c["key"])] = slot
+                        c["stage"].itform = True
+                    used.setdefault(slot, set()).update(need)
+                    st.targets[(part, key)] = (slot, qmap)
+                    st.itform = True
+            cand += mine                            # sources for later stages only
+        # per-row operands of one-trip parts: loaded before the first stage
+        n = 0
+        for si, st in enumerate(self.stages):
+            one = st.form == "block" or (st.form in ("map", "serial") and st.trips == 1)
+            if not one or st.split is None:
+                continue
+            for ld in st.parts()["stmts"]:
+                key = ld.key()
+                if (n >= self.HOIST or key in st.hoisted or ("stmts", key) in st.targets
+                        or ("stmts", key) in st.sources or not self.reusable(st, ld, "stmts")):
+                    continue
+                st.hoisted[key] = (f"hz{n}", ld)
+                n += 1
 
     def grid(self):
         return self.blocks, self.threads
@@ -1042,32 +1272,45 @@ class RowBlockPlan(Plan):
                 em.emit(f"if ({guard}) {line}" if guard else line)
             em.reset_memo()
 
+    def lane_loop(self, em, st: RowStage, var: str, stride: int, start: str = "threadIdx.x") -> None:
+        """The loop of a lane over its share of the stage's index (`var` < N, in steps of stride);
+        with itform, a counted loop (it_) whose trips index the forwarding registers."""
+        if st.itform:
+            em.emit("#pragma unroll")
+            em.emit(f"for (int it_ = 0; it_ < {st.trips}; it_++) {{")
+            em.emit(f"    const uint32_t {var} = {start} + {stride}u * (uint32_t)it_;")
+            if st.N % stride:
+                em.emit(f"    if ({var} >= {st.N}u) break;")
+            return
+        trips = -(-st.N // stride)
+        if trips > 1:
+            em.emit(f"#pragma unroll {min(4, trips)}")
+        em.emit(f"for (uint32_t {var} = {start}; {var} < {st.N}u; {var} += {stride}u) {{")
+
     def source(self) -> str:
         T = self.threads
         body: list[str] = []
         shared: list[str] = []
-        for si, k in enumerate(self.kernels):
+        self.qtables = []
+        for si, (k, st) in enumerate(zip(self.kernels, self.stages)):
             sc = RowBlockScope(self)
             sc.stream_name = self.stream_param(k)
+            sc.targets, sc.sources = st.targets, st.sources
+            sc.hoisted = {key: name for key, (name, ld) in st.hoisted.items()}
             em = Emitter(sc, body, "        ")
             sc.em = em
-            E = ir.prod(v.extent for v in k.domain) // self.R
+            E, n, red = st.E, st.n, k.red
             sc.rand = f"(row * {E}u + e)"
-            red = k.red
-            n = ir.prod(v.extent for v in red.vars) if red is not None else 1
             em.emit(f"// stage {si}: {k.name} ({E} per row" + (f", reduce {red.op} of {n}" if red else "") + ")")
-            if red is not None and red.op in RED_CODE and E <= 16 and n >= 256:
-                self.block_stage(em, sc, k, si, E, n, shared)
+            if st.form == "block":
+                self.block_stage(em, sc, st, si, shared)
                 em.emit("__syncthreads();")
                 continue
-            wave = red is not None and red.op in RED_CODE and E < 64 and n > 64
-            trips = -(-E // (T // 64 if wave else T))          # outputs per wave / per lane
-            if trips > 1:
-                em.emit(f"#pragma unroll {min(4, trips)}")
+            wave = st.form == "wave"
             if wave:
                 em.emit(f"for (uint32_t e = threadIdx.x >> 6; e < {E}u; e += {T // 64}u) {{")
             else:
-                em.emit(f"for (uint32_t e = threadIdx.x; e < {E}u; e += {T}u) {{")
+                self.lane_loop(em, st, "e", T)
             em.ind += "    "
             for line in decode(k.domain, f"row * {E}u + e", "uint32_t"):
                 em.emit(line)
@@ -1092,24 +1335,55 @@ class RowBlockPlan(Plan):
                 em.emit(f"acc = anvil_wave_all<{RED_CODE[red.op]}, {ty}>(acc);")
                 self.stage_statements(em, k, sc, guard="lane == 0")
             else:
+                strides = ir.row_major_strides([v.extent for v in red.vars])
+                sc.red_index = " + ".join(f"{s} * v{v.id}" if s != 1 else f"v{v.id}"
+                                          for v, s in zip(red.vars, strides)) or "0"
+                sc.part = "body"
                 serial_reduction(em, sc, k, em.ind, unroll=True)
+                sc.part = "stmts"
                 self.stage_statements(em, k, sc)
             em.ind = em.ind[:-4]
             em.emit("}")
             em.emit("__syncthreads();")
         for bid, S in self.shadow.items():
             shared.append(f"    __shared__ {ctype(self.gen.by_id[bid].dtype)} sh{bid}[{S}];")
-        head = [self.comment() + f" · one workgroup per row, {self.R} rows", self.header(T)] + shared + [
+        tables = [f"    constexpr int {name}[{len(qmap)}] = {{{', '.join(map(str, qmap))}}};"
+                  for name, qmap in self.qtables]
+        prologue = self.row_prologue()          # before the header: its loads add parameters
+        head = [self.comment() + f" · one workgroup per row, {self.R} rows", self.header(T)] + shared + tables + [
                 "    const uint32_t lane = threadIdx.x & 63u;",
                 "    (void)lane;",
                 f"    for (uint32_t row = blockIdx.x; row < {self.R}u; row += gridDim.x) {{"]
-        return "\n".join(head + body + ["    }", "}"])
+        return "\n".join(head + prologue + body + ["    }", "}"])
 
-    def block_stage(self, em, sc, k, si, E, n, shared):
+    def row_prologue(self) -> list[str]:
+        """Declarations of the forwarding registers, and the hoisted loads, at the top of a row."""
+        out: list[str] = []
+        for slot, (ty, trips, I) in enumerate(self.slots):
+            out.append(f"        {ty} fw{slot}[{trips}][{I}];")
+        for si, st in enumerate(self.stages):
+            for key, (name, ld) in st.hoisted.items():
+                sc = RowBlockScope(self)
+                em = Emitter(sc, out, "        ", prefix=f"p{name}_")
+                sc.em = em
+                ty = ctype(ld.dtype)
+                em.emit(f"{ty} {name} = {'0.0f' if ty == 'float' else '0'};")
+                em.emit(f"if (threadIdx.x < {st.E}u) {{      // stage {si}'s lanes")
+                em.ind += "    "
+                em.emit("const uint32_t e = threadIdx.x;")
+                for line in decode(st.k.domain, f"row * {st.E}u + e", "uint32_t"):
+                    em.emit(line)
+                em.emit(f"{name} = {em.build(ld)};")
+                em.ind = em.ind[:-4]
+                em.emit("}")
+        return out
+
+    def block_stage(self, em, sc, st: RowStage, si, shared):
         """Every lane accumulates its share of the reduction for each of the E outputs; wave
         shuffles, then LDS across the four waves (in wave order), give the sums; lane e finishes
         output e."""
         T = self.threads
+        k, E, n = st.k, st.E, st.n
         red = k.red
         dt = red.body.dtype
         ty = ctype(dt)
@@ -1118,16 +1392,21 @@ class RowBlockPlan(Plan):
         em.ind += "    "
         em.emit(f"{ty} acc[{E}];")
         em.emit(f"for (int q = 0; q < {E}; q++) acc[q] = {red_init(red.op, dt)};")
-        em.emit("#pragma unroll 4")
-        em.emit(f"for (uint32_t j = threadIdx.x; j < {n}u; j += {T}u) {{")
+        if st.itform:
+            self.lane_loop(em, st, "j", T)
+        else:
+            em.emit("#pragma unroll 4")
+            em.emit(f"for (uint32_t j = threadIdx.x; j < {n}u; j += {T}u) {{")
         em.ind += "    "
         for line in decode(list(red.vars), "j", "uint32_t"):
             em.emit(line)
+        sc.part = "body"
         for q in range(E):
             em.emit("{")
             em.ind += "    "
             saved = em.memo
             em.memo = {}
+            sc.q = q
             em.emit(f"const uint32_t e = {q}u;")
             for line in decode(k.domain, f"row * {E}u + e", "uint32_t"):
                 em.emit(line)
@@ -1136,6 +1415,7 @@ class RowBlockPlan(Plan):
             em.memo = saved
             em.ind = em.ind[:-4]
             em.emit("}")
+        sc.part = "stmts"
         em.ind = em.ind[:-4]
         em.emit("}")
         em.emit(f"for (int q = 0; q < {E}; q++) {{")

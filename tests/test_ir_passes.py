@@ -84,3 +84,71 @@ def test_split_vars_is_the_row_major_index():
     st = k2.stmts[0]
     assert st.offset == ir.Affine(0, {i: 12, a: 4, b: 1})
     assert st.value.offset == ir.Affine(3, {a: 20, b: 5})
+
+
+def row_block_plans(name):
+    from anvil.backend import hip
+    prog, data = load_ir(name)
+    gen = hip.HipGen(prog, seed=int(data.get("seed", 0)))
+    gen.generate()
+    out = []
+    for p in gen.plans:
+        for q in getattr(p, "parts", [p]):
+            if q.kind == "rowblock":
+                out.append(q)
+    return out
+
+
+def lane_addresses(plan, st, ld, part, rows):
+    """The element each (row, lane, trip, inner index) of a row-block stage loads, by decoding the
+    flat index row·E + e over the whole domain (as the generated code does)."""
+    T = plan.threads
+    k = st.k
+    rows = np.asarray(rows)[:, None, None, None]
+    idx = np.arange(T)[None, :, None, None] + T * np.arange(st.trips)[None, None, :, None]
+
+    def digits(flat, vars_):
+        strides = ir.row_major_strides([v.extent for v in vars_])
+        return {v: (flat // s) % v.extent for v, s in zip(vars_, strides)}
+    if st.form == "block":
+        vals = digits(rows * st.E + np.arange(st.E)[None, None, None, :], k.domain)
+        vals.update(digits(idx, k.red.vars))
+    else:
+        vals = digits(rows * st.E + idx, k.domain)
+        if part == "body":
+            vals.update(digits(np.arange(st.n)[None, None, None, :], k.red.vars))
+    addr = ld.offset.const + sum(c * vals[v] for v, c in ld.offset.terms.items())
+    return np.broadcast_to(addr + 0 * idx, np.broadcast_shapes(np.shape(addr), idx.shape)), idx < st.N
+
+
+def test_row_block_forwarding_reads_the_same_elements():
+    """Every operand a row-block stage takes from registers (loaded by an earlier stage of the same
+    lane and trip) is the element that stage would load itself: checked against a decode of the
+    whole flat index, for every row, lane and trip. C2's block forwards W3 and h2 from the logits
+    stage to the input-gradient stages and hoists the bias and label loads."""
+    total = 0
+    for name in ["c2_wide_mlp", "c1_mlp", "c4_transformer", "c5_small", "mnist_like", "attention_train"]:
+        for plan in row_block_plans(name):
+            slots = {}
+            for st in plan.stages:
+                for (part, key), slot in st.sources.items():
+                    slots[slot] = (st, part, key)
+            for t, st in enumerate(plan.stages):
+                for (part, key), (slot, qmap) in st.targets.items():
+                    src, spart, skey = slots[slot]
+                    assert plan.stages.index(src) < t
+                    ld = next(x for x in st.parts()[part] if x.key() == key)
+                    ld2 = next(x for x in src.parts()[spart] if x.key() == skey)
+                    assert ld.buf.root is ld2.buf.root and ld.buf.root.id not in plan.chain_writes
+                    rows = range(plan.R) if plan.R <= 512 else [0, 1, 2, plan.R // 2, plan.R - 1]
+                    a, act = lane_addresses(plan, st, ld, part, rows)
+                    b, act2 = lane_addresses(plan, src, ld2, spart, rows)
+                    b = b[:, :, :st.trips, :][..., qmap]
+                    act2 = act2[:, :, :st.trips, :]
+                    assert (act2 | ~act).all()
+                    assert ((a == b) | ~act).all(), (name, plan.name, t, key)
+                    total += 1
+            if name == "c2_wide_mlp":
+                assert sum(len(st.targets) for st in plan.stages) == 2
+                assert sum(len(st.hoisted) for st in plan.stages) == 2
+    assert total >= 30
