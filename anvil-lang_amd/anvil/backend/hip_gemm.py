@@ -557,7 +557,20 @@ class GemmPlan(Plan):
             S = max(2, min(1024 // tiles, s.K // 512))
             self.kslice = -(-(-(-s.K // S)) // 8) * 8
             self.kslices = -(-s.K // self.kslice)
-        nch = -(-(self.kslice // 8) // self.waves)          # chunks per wave
+        # chunks of 8·G k (anvil_mm_tile_kpipe): two 16-byte loads per lane of an operand contiguous
+        # in k (half a cache line of each row) when each wavefront has K ≥ 128 to cover (measured:
+        # C2's 256 x 1024 x 1024 products 9.7 -> 8.6 µs, C4's weight gradients with K = 4096 in
+        # slices of 512 96 -> 86 µs; with K = 64 per wavefront, fewer and larger chunks were up to
+        # 3 µs slower), while the registers in flight stay within 64 per lane
+        self.kgroup = 1
+        plain = {self.amode, self.bmode} <= {"ANVIL_LD_KC", "ANVIL_LD_RC"}
+        for g in (4, 2):
+            if (self.pipe and plain and g <= int(os.environ.get("ANVIL_GEMM_KGROUP", "2"))
+                    and s.K % (8 * g) == 0 and self.kslice % (8 * g) == 0
+                    and self.kslice // self.waves >= 128 and 2 * (self.ptm + self.ptn) * 4 * g <= 64):
+                self.kgroup = g
+                break
+        nch = -(-(self.kslice // (8 * self.kgroup)) // self.waves)      # chunks per wave
         self.depth = max(1, min(int(os.environ.get("ANVIL_GEMM_DEPTH", "2" if nch <= 32 else "4")), nch))
         self.threads = 64 * self.waves if self.sched == "ksplit" else 256
         self.tm = -(-s.M // self.BM)
@@ -859,10 +872,11 @@ class GemmPlan(Plan):
                 b_ks = s.b_ks if not s.k_multi else s.k_multi[-1][2]
                 kargs = (f"pa, arow, ak, {a_ks}LL, pb, brow, bk, {b_ks}LL, {s.M}, {s.N}, m0, n0, {krange}, "
                          "opa, opb")
-                nch = -(-(self.kslice // 8) // W)
+                G = self.kgroup
+                nch = -(-(self.kslice // (8 * G)) // W)
                 main = [f"    float part[{TM}][{TN}][{16 // W}];",
                         f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
-                        f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}>(part, {kargs});"]
+                        f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}, {G}>(part, {kargs});"]
             else:
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]

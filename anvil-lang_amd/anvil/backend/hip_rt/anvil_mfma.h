@@ -295,11 +295,15 @@ __device__ __forceinline__ void anvil_mm_tile_ksplit(float (&out)[TM][TN][16 / W
             }
 }
 
-// The same K split with a software pipeline (K a multiple of 8): the K range is cut into C 8-k
-// chunks, NCH consecutive ones per wave (the last busy wave may have fewer, later waves none). A
-// wave keeps D chunks of operands in flight: it waits only for the oldest, runs its 4 MFMAs, and
+// The same K split with a software pipeline (K a multiple of 8G): the K range is cut into C chunks
+// of 8G k, NCH consecutive ones per wave (the last busy wave may have fewer, later waves none). A
+// wave keeps D chunks of operands in flight: it waits only for the oldest, runs its 4G MFMAs, and
 // reuses those registers for the chunk D ahead, so the matrix cores start on the first data to
-// arrive instead of after the last. The chunk loop is unrolled (NCH is a compile-time constant):
+// arrive instead of after the last. In a chunk, lane (r, h) holds k0 + 4G·h + s (s < 4G) of its
+// row r, and MFMA s pairs k0 + s with k0 + 4G + s: an operand contiguous in k is read with G
+// 16-byte loads per lane, so with G = 4 the two half-waves cover 128 bytes, a whole cache line, of
+// each of the 32 rows (G = 1: a quarter line per row and load, the other quarters coming in later
+// chunks after the line may have left the L1). The chunk loop is unrolled (NCH is a compile-time constant):
 // straight-line code, where the compiler's wait counts are exact. Rows and columns past M / N are
 // zero (CHKM, CHKN: the tile may cross the edge); k is always in range. Where row (column) t of
 // an operand starts is arow(t) (brow(t)): t times its stride, or, for rows picked through an index
@@ -333,8 +337,8 @@ struct anvil_all_pred {
     __device__ __forceinline__ bool operator()(int, int) const { return true; }
 };
 
-template <int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, bool FULL, class AK, class BK,
-          class OPA, class OPB, class APRED, class BPRED>
+template <int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, bool FULL, int G, class AK,
+          class BK, class OPA, class OPB, class APRED, class BPRED>
 __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
                                                     const float *__restrict__ a, const long long (&ao)[TM], AK ak,
                                                     long long a_ks, const float *__restrict__ b,
@@ -342,19 +346,21 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
                                                     int M, int N, int m0, int n0, int c0, int n, OPA opa, OPB opb,
                                                     APRED apred, BPRED bpred) {
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
-    float ab[D][TM][4], bb[D][TN][4];
+    float ab[D][TM][4 * G], bb[D][TN][4 * G];
 #define ANVIL_KP_LOAD(d, c)                                                                                \
     if (FULL || (c) < n) {                                                                                 \
-        const int k_ = 8 * (c0 + (c)) + 4 * h;                                                             \
-        long long ka_[4], kb_[4];                                                                          \
-        anvil_koffs<AMODE>(ak, k_, a_ks, ka_);                                                             \
-        anvil_koffs<BMODE>(bk, k_, b_ks, kb_);                                                             \
-        _Pragma("unroll") for (int i = 0; i < TM; i++)                                                     \
-            anvil_chunk_load_k<AMODE, CHKM>(ab[d][i], a, ao[i], ka_, m0 + 32 * i + r, M,                  \
-                                            apred(m0 + 32 * i + r, k_));                                   \
-        _Pragma("unroll") for (int j = 0; j < TN; j++)                                                     \
-            anvil_chunk_load_k<BMODE, CHKN>(bb[d][j], b, bo[j], kb_, n0 + 32 * j + r, N,                  \
-                                            bpred(n0 + 32 * j + r, k_));                                   \
+        _Pragma("unroll") for (int g = 0; g < G; g++) {                                                    \
+            const int k_ = 8 * G * (c0 + (c)) + 4 * G * h + 4 * g;                                        \
+            long long ka_[4], kb_[4];                                                                      \
+            anvil_koffs<AMODE>(ak, k_, a_ks, ka_);                                                         \
+            anvil_koffs<BMODE>(bk, k_, b_ks, kb_);                                                         \
+            _Pragma("unroll") for (int i = 0; i < TM; i++)                                                 \
+                anvil_chunk_load_k<AMODE, CHKM>(*reinterpret_cast<float(*)[4]>(&ab[d][i][4 * g]), a, ao[i], \
+                                                ka_, m0 + 32 * i + r, M, apred(m0 + 32 * i + r, k_));       \
+            _Pragma("unroll") for (int j = 0; j < TN; j++)                                                 \
+                anvil_chunk_load_k<BMODE, CHKN>(*reinterpret_cast<float(*)[4]>(&bb[d][j][4 * g]), b, bo[j], \
+                                                kb_, n0 + 32 * j + r, N, bpred(n0 + 32 * j + r, k_));       \
+        }                                                                                                  \
     }
 #pragma unroll
     for (int c = 0; c < D; c++) ANVIL_KP_LOAD(c, c)
@@ -363,7 +369,7 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
     for (int c = 0; c < NCH; c++) {
         if (FULL || c < n) {
 #pragma unroll
-            for (int s = 0; s < 4; s++)
+            for (int s = 0; s < 4 * G; s++)
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -377,8 +383,9 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
 #undef ANVIL_KP_LOAD
 }
 
-template <int W, int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, class AROW, class BROW,
-          class AK, class BK, class OPA, class OPB, class APRED = anvil_all_pred, class BPRED = anvil_all_pred>
+template <int W, int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, int G = 1, class AROW,
+          class BROW, class AK, class BK, class OPA, class OPB, class APRED = anvil_all_pred,
+          class BPRED = anvil_all_pred>
 __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W],
                                                     const float *__restrict__ a, AROW arow, AK ak, long long a_ks,
                                                     const float *__restrict__ b, BROW brow, BK bk, long long b_ks,
@@ -388,7 +395,7 @@ __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W]
     __shared__ float part[W * TM * TN * 16 * 64];
     const int lane = threadIdx.x & 63, r = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     // uniform: scalar branches
-    const int c0 = (kbeg >> 3) + w * NCH, n = min(NCH, max(0, ((kbeg + K) >> 3) - c0));
+    const int c0 = kbeg / (8 * G) + w * NCH, n = min(NCH, max(0, (kbeg + K) / (8 * G) - c0));
     long long ao[TM], bo[TN];
 #pragma unroll
     for (int i = 0; i < TM; i++) ao[i] = (!CHKM || m0 + 32 * i + r < M) ? arow(m0 + 32 * i + r) : 0;
@@ -397,11 +404,11 @@ __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W]
     anvil_mm_acc<TM, TN> acc;
     acc.zero();
     if (n == NCH)
-        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, true>(acc, a, ao, ak, a_ks, b, bo, bk, b_ks, M, N,
-                                                                            m0, n0, c0, n, opa, opb, apred, bpred);
+        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, true, G>(acc, a, ao, ak, a_ks, b, bo, bk, b_ks, M,
+                                                                               N, m0, n0, c0, n, opa, opb, apred, bpred);
     else if (n > 0)
-        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, false>(acc, a, ao, ak, a_ks, b, bo, bk, b_ks, M,
-                                                                             N, m0, n0, c0, n, opa, opb, apred, bpred);
+        anvil_mm_wave_kpipe<TM, TN, AMODE, BMODE, NCH, D, CHKM, CHKN, false, G>(acc, a, ao, ak, a_ks, b, bo, bk, b_ks, M,
+                                                                                N, m0, n0, c0, n, opa, opb, apred, bpred);
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll

@@ -43,7 +43,9 @@ def test_gpu_full_size_program_matches_reference(name):
     to 2 %; measured 0.09 %, and 0.12 % / 0.9 % at the worst tensor).
     C1 (784-128-10 MLP, SGD, batch 64, one epoch and the test accuracy): the printed loss and
     accuracy and the last layer's trained weights. C2 (784-1024-1024-10 MLP, Adam, batch 256, 500
-    steps over 65,536 samples): the printed loss. C2 for 10 steps at full size: the printed loss and
+    steps over 65,536 samples): the printed loss, to 2e-3 (the last batch's loss after 500 Adam
+    steps depends on the order of every sum before it: the same kernels summing K in 8-k or 16-k
+    chunks printed 2.3053, 2.3026 and 2.3072 against the reference's 2.3037). C2 for 10 steps at full size: the printed loss and
     trained weights and biases, measured against how far Adam moves a parameter (at most about lr
     per step, whatever its gradient's size: a gradient that crosses zero near a step takes a full
     step either way, so summing the batch in another order — the matrix cores' vs NumPy's — moves
@@ -57,7 +59,7 @@ def test_gpu_full_size_program_matches_reference(name):
     rc, out, err, arrays = run_program(name, emulate=False, keep=keep, timeout=300)
     assert rc == 0, err
     z = vectors(name)
-    problem = outputs_match(stdout_of(z), out, rtol=1e-3)
+    problem = outputs_match(stdout_of(z), out, rtol=2e-3 if name == "c2_full" else 1e-3)
     assert problem is None, problem
     for k in keep:
         ref, got = z[f"buf:{k}"].astype(np.float64), arrays[k].astype(np.float64)
