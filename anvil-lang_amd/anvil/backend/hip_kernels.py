@@ -995,13 +995,7 @@ class RowBlockScope(KernelScope):
         got = self.targets.get((self.part, key))
         if got is not None:
             slot, qmap = got
-            if len(set(qmap)) == 1:
-                q = str(qmap[0])
-            elif qmap == list(range(len(qmap))):
-                q = self.red_index
-            else:
-                q = f"fwq{slot}_{len(self.plan.qtables)}[{self.red_index}]"
-                self.plan.qtables.append((q.split("[")[0], qmap))
+            q = str(qmap[0]) if len(set(qmap)) == 1 else self.red_index      # one element, or the same index
             return f"fw{slot}[it_][{q}]"
         return super().override_load(ld)
 
@@ -1130,7 +1124,6 @@ class RowBlockPlan(Plan):
                 if dead:
                     self.dead.add(b.id)
         self.stages = [RowStage(k, R, self.threads) for k in kernels]
-        self.qtables: list = []
         self.plan_reuse()
 
     # ------------------------------------------------------------------ operand reuse
@@ -1214,7 +1207,8 @@ class RowBlockPlan(Plan):
                             if not ok.any():
                                 break
                             qmap.append(int(np.argmax(ok)))
-                        if len(qmap) == I:
+                        # the register is the same element for every index, or the index itself
+                        if len(qmap) == I and (len(set(qmap)) == 1 or qmap == list(range(I))):
                             match = (c, qmap)
                             break
                     if match is None:
@@ -1291,7 +1285,6 @@ class RowBlockPlan(Plan):
         T = self.threads
         body: list[str] = []
         shared: list[str] = []
-        self.qtables = []
         for si, (k, st) in enumerate(zip(self.kernels, self.stages)):
             sc = RowBlockScope(self)
             sc.stream_name = self.stream_param(k)
@@ -1347,10 +1340,8 @@ class RowBlockPlan(Plan):
             em.emit("__syncthreads();")
         for bid, S in self.shadow.items():
             shared.append(f"    __shared__ {ctype(self.gen.by_id[bid].dtype)} sh{bid}[{S}];")
-        tables = [f"    constexpr int {name}[{len(qmap)}] = {{{', '.join(map(str, qmap))}}};"
-                  for name, qmap in self.qtables]
         prologue = self.row_prologue()          # before the header: its loads add parameters
-        head = [self.comment() + f" · one workgroup per row, {self.R} rows", self.header(T)] + shared + tables + [
+        head = [self.comment() + f" · one workgroup per row, {self.R} rows", self.header(T)] + shared + [
                 "    const uint32_t lane = threadIdx.x & 63u;",
                 "    (void)lane;",
                 f"    for (uint32_t row = blockIdx.x; row < {self.R}u; row += gridDim.x) {{"]
