@@ -125,7 +125,9 @@ def test_row_block_forwarding_reads_the_same_elements():
     """Every operand a row-block stage takes from registers (loaded by an earlier stage of the same
     lane and trip) is the element that stage would load itself: checked against a decode of the
     whole flat index, for every row, lane and trip. C2's block forwards W3 and h2 from the logits
-    stage to the input-gradient stages and hoists the bias and label loads."""
+    stage to the input-gradient stages and hoists the bias and label loads. Loads that a block stage
+    makes as one vector for several outputs read consecutive, aligned elements (C2: W3's row j as
+    5 8-byte loads)."""
     total = 0
     for name in ["c2_wide_mlp", "c1_mlp", "c4_transformer", "c5_small", "mnist_like", "attention_train"]:
         for plan in row_block_plans(name):
@@ -148,7 +150,18 @@ def test_row_block_forwarding_reads_the_same_elements():
                     assert (act2 | ~act).all()
                     assert ((a == b) | ~act).all(), (name, plan.name, t, key)
                     total += 1
+            for st in plan.stages:
+                for key, (vname, w, ld) in getattr(st, "vectors", {}).items():
+                    # one w-wide load per w outputs: consecutive elements from a w-aligned first one
+                    rows = range(plan.R) if plan.R <= 512 else [0, 1, 2, plan.R // 2, plan.R - 1]
+                    a, act = lane_addresses(plan, st, ld, "body", rows)
+                    q = np.arange(st.E)
+                    assert ((a == a[..., :1] + q) | ~act).all(), (name, plan.name, key)
+                    assert ((a[..., 0] % w == 0) | ~act[..., 0]).all(), (name, plan.name, key)
+                    assert ld.buf.root.kind not in ir.EXTERN_KINDS
+                    total += 1
             if name == "c2_wide_mlp":
+                assert [w for st in plan.stages for (_, w, _) in getattr(st, "vectors", {}).values()] == [2]
                 assert sum(len(st.targets) for st in plan.stages) == 2
                 assert sum(len(st.hoisted) for st in plan.stages) == 2
     assert total >= 30
