@@ -21,6 +21,7 @@ Each plan produces the kernel's source and the host-side launch: grid, block and
 """
 from __future__ import annotations
 
+import os
 import re
 
 from .. import ir
@@ -543,7 +544,16 @@ class RowsPlan(Plan):
         self.threads = THREADS if lanes > 1 else min(THREADS, max(64, 64 * -(-self.R // 64)))
         if lanes == 1:
             self.rpb = self.threads
-        self.blocks = max(1, min(-(-self.R // self.rpb), MAX_BLOCKS))
+        # rows within one wavefront: sixteen wavefronts per CU (four per SIMD) when that gives each
+        # wavefront two rows (C3's layernorm over 8192 rows of 1024: 2048 workgroups 12.3 µs, 1024
+        # 11.8 µs, 512 12.9; four rows each of 256 (C4's) measured no better). A row spread over a
+        # workgroup (its reductions cross the wavefronts through LDS) keeps one workgroup per row:
+        # C3's softmax over rows of 4096 was 42.6 µs so and 45-47 µs with the cap.
+        want = -(-self.R // self.rpb)
+        cap = int(os.environ.get("ANVIL_ROWS_BLOCKS", str(16 * 256 * 64 // self.threads)))
+        if 1 < lanes <= 64 and want <= 2 * cap:
+            want = min(want, cap)
+        self.blocks = max(1, min(want, MAX_BLOCKS))
         self.cached = self.Q <= QMAX and (lanes > 1 or self.n <= 32)
         self.cache_arrays: dict = {}       # canonical key -> array name
         self.emulate = emulate
