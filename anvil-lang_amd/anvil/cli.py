@@ -9,7 +9,7 @@ These mirror the reference's `anvil cuda file.anvil` and `anvil run|build --cuda
 305-320): the same generated-file / build / run split, libraries cached by the hash of their source
 (cli.py:127-136; $ANVIL_CACHE picks the directory). The reference's front end turns .anvil source
 into the IR; this package starts from the IR (see `irjson`), which the reference front end can
-write, and which the reference's own cli.py hands to `hip.generate` directly.
+write, and which the reference's own cli.py can hand to `hip.generate` directly.
 
 `run` executes the program's `anvil_main` in this process: its stdout is the program's, a run-time
 error prints `anvil: runtime error: ...` and exits with status 1, as a compiled Anvil program does.

@@ -281,8 +281,8 @@ def main() -> int:
         print(json.dumps(c3_run(20)), flush=True)
         return 0
     if args.gpus != 1:
-        print(f"bench: this build measures one GPU only (asked for {args.gpus}); the multi-GPU design is "
-              "described in DESIGN.md and is not run", file=sys.stderr)
+        print(f"bench: this build measures one GPU only (asked for {args.gpus}); data-parallel sharding "
+              "over several GPUs is designed but not run", file=sys.stderr)
         return 2
     prog, data = load_program()
     ms, wall, prof, lib = gpu_run(prog, data, args.steps, args.warmup, graphs=args.graphs)
