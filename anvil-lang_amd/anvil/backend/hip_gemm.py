@@ -561,15 +561,15 @@ class GemmPlan(Plan):
         # in k (half a cache line of each row) when each wavefront has K ≥ 128 to cover (measured:
         # C2's 256 x 1024 x 1024 products 9.7 -> 8.6 µs, C4's weight gradients with K = 4096 in
         # slices of 512 96 -> 86 µs; with K = 64 per wavefront, fewer and larger chunks were up to
-        # 3 µs slower), while the registers in flight stay within 64 per lane ($ANVIL_GEMM_KREGS;
-        # C3's one-wavefront 2 x 4 tile with G = 2 needs 96: 128-132 TFLOP/s either way)
+        # 3 µs slower), while the registers in flight stay within 96 per lane ($ANVIL_GEMM_KREGS):
+        # C3's one-wavefront 2 x 4 tile takes G = 2 with 96, 129.2 -> 131.7 TFLOP/s (three runs each)
         self.kgroup = 1
         plain = {self.amode, self.bmode} <= {"ANVIL_LD_KC", "ANVIL_LD_RC"}
         for g in (4, 2):
             if (self.pipe and plain and g <= int(os.environ.get("ANVIL_GEMM_KGROUP", "2"))
                     and s.K % (8 * g) == 0 and self.kslice % (8 * g) == 0
                     and self.kslice // self.waves >= 128
-                    and 2 * (self.ptm + self.ptn) * 4 * g <= int(os.environ.get("ANVIL_GEMM_KREGS", "64"))):
+                    and 2 * (self.ptm + self.ptn) * 4 * g <= int(os.environ.get("ANVIL_GEMM_KREGS", "96"))):
                 self.kgroup = g
                 break
         nch = -(-(self.kslice // (8 * self.kgroup)) // self.waves)      # chunks per wave
