@@ -976,7 +976,8 @@ class RowBlockBuilder:
 
 class RowBlockScope(KernelScope):
     """Loads of the chain's own row slices kept in LDS read the LDS copy; operands the plan keeps
-    in registers (hoisted per-row loads, values forwarded from an earlier stage) read those."""
+    in registers (hoisted per-row loads, values forwarded from an earlier stage, the components of
+    a vector load a block stage's outputs share) read those."""
 
     def __init__(self, plan):
         super().__init__(plan)
