@@ -1066,7 +1066,16 @@ def generate(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bo
         graphs = os.environ.get("ANVIL_HIP_GRAPHS", "0") == "1"
     if check not in (None, "nan", "inf"):
         raise ValueError(f"check must be None, 'nan' or 'inf', not {check!r}")
-    return HipGen(prog, seed=seed, library=library, emulate=emulate, graphs=graphs, check=check).generate()
+    # the IR passes make new loop variables, whose ids name them in the source: start those right
+    # after the program's own ids, so that one program gives one source (and one library name) in
+    # any process, whatever that process loaded or generated before
+    after = getattr(prog, "max_id", None)
+    resume = ir.restart_ids(after) if after is not None else None
+    try:
+        return HipGen(prog, seed=seed, library=library, emulate=emulate, graphs=graphs, check=check).generate()
+    finally:
+        if resume is not None:
+            ir.bump_ids(resume - 1)
 
 
 def hipcc() -> str:

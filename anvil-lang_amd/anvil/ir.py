@@ -38,6 +38,15 @@ def bump_ids(at_least: int) -> None:
     _next_id = itertools.count(max(cur, at_least + 1))
 
 
+def restart_ids(after: int) -> int:
+    """Make the next fresh id after + 1, whatever was allocated before; returns the id that would
+    have come next (give it back to bump_ids to keep ids unique across programs afterwards)."""
+    global _next_id
+    cur = next(_next_id)
+    _next_id = itertools.count(after + 1)
+    return cur
+
+
 def prod(xs) -> int:
     out = 1
     for x in xs:

@@ -370,6 +370,7 @@ def load(data) -> "ir.Program":
     prog = ir.Program(main, [bufs[i] for i in sorted(bufs)],
                       None if data.get("source") is None else _Source(data["source"]))
     ir.bump_ids(max_id)
+    prog.max_id = max_id                # the largest id the program holds (see hip.generate)
     return prog
 
 
