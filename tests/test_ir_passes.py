@@ -165,3 +165,16 @@ def test_row_block_forwarding_reads_the_same_elements():
                 assert sum(len(st.targets) for st in plan.stages) == 2
                 assert sum(len(st.hoisted) for st in plan.stages) == 2
     assert total >= 30
+
+
+def test_generated_source_does_not_depend_on_earlier_programs():
+    """The passes' new loop variables are named by ids that follow the program's own, so the same
+    program gives the same source (and library name) after other programs were generated in the
+    same process, as in a build pool."""
+    from anvil.backend import hip
+    prog, data = load_ir("c5_small")
+    alone = hip.generate(prog, seed=int(data.get("seed", 0)))
+    other, odata = load_ir("c4_small")
+    hip.generate(other, seed=int(odata.get("seed", 0)))
+    again, _ = load_ir("c5_small")
+    assert hip.generate(again, seed=int(data.get("seed", 0))) == alone
