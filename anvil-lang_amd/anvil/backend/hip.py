@@ -116,9 +116,11 @@ class HipGen:
         if not emulate and not check and os.environ.get("ANVIL_HIP_GATHER_FWD", "1") != "0":
             from . import hip_gemm
             prog = hip_gemm.forward_gather_copies(prog, A.host_scalars(prog))
+        # the loop variables the passes add take ids after the program's own
+        self.ids = A.IdSource(prog)
         if not check and os.environ.get("ANVIL_HIP_IMPLICIT_CONV", "1") != "0":
             from . import hip_conv
-            prog = hip_conv.forward_im2col_copies(prog)
+            prog = hip_conv.forward_im2col_copies(prog, self.ids)
         self.prog = prog
         self.seed = seed & 0xFFFFFFFF
         self.library = library
@@ -631,8 +633,11 @@ class HipGen:
         span = k.span
         if span is not None and span.location():
             head += f" at {span.location()}"
-            if getattr(span, "src", None):
-                line = "\n      " + span.src
+            text = getattr(span, "src", None)
+            if text is None and getattr(span, "file", None) is not None:
+                text = span.file.line_text(span.line).strip()      # a front-end span (source.py)
+            if text:
+                line = "\n      " + text
         return f"{head}:{line}\n  computing ({k.name}):  {ir.fmt_kernel(k)}"
 
     def segment(self, seg: list, ind: str) -> list[str]:
@@ -868,7 +873,8 @@ class HipGen:
             if r.init is not None and r.id in self.device_bufs:
                 self.mirror(r)
         HSD_ID = 900_000_003
-        self.device_bufs[HSD_ID] = Buffer("host_scalars.device_copy", (max(1, len(self.hsd)),), I32, "scratch", id=HSD_ID)
+        self.device_bufs[HSD_ID] = A.new_buffer(HSD_ID, "host_scalars.device_copy", (max(1, len(self.hsd)),), I32,
+                                                "scratch")
         dev = sorted(self.device_bufs.values(), key=lambda b: b.id)
         plan = A.plan_arena(self.prog, dev, self.full_writer, share=os.environ.get("ANVIL_HIP_SHARE", "1") != "0",
                             fused=self.fused_group)
@@ -1066,16 +1072,7 @@ def generate(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bo
         graphs = os.environ.get("ANVIL_HIP_GRAPHS", "0") == "1"
     if check not in (None, "nan", "inf"):
         raise ValueError(f"check must be None, 'nan' or 'inf', not {check!r}")
-    # the IR passes make new loop variables, whose ids name them in the source: start those right
-    # after the program's own ids, so that one program gives one source (and one library name) in
-    # any process, whatever that process loaded or generated before
-    after = getattr(prog, "max_id", None)
-    resume = ir.restart_ids(after) if after is not None else None
-    try:
-        return HipGen(prog, seed=seed, library=library, emulate=emulate, graphs=graphs, check=check).generate()
-    finally:
-        if resume is not None:
-            ir.bump_ids(resume - 1)
+    return HipGen(prog, seed=seed, library=library, emulate=emulate, graphs=graphs, check=check).generate()
 
 
 def hipcc() -> str:

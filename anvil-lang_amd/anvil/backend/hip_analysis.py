@@ -33,6 +33,45 @@ _UNSHARED = set(filter(None, __import__("os").environ.get("ANVIL_HIP_UNSHARED", 
 SHARED_KINDS = ("temp", "grad")
 
 
+# ----------------------------------------------------------------------------- ids of added objects
+
+class IdSource:
+    """Ids for the loop variables and scratch buffers the backend adds to a program. Ids name
+    variables and buffers in the generated source, so they are counted up from the program's own
+    largest id: one program always gives one source (and one library name), whatever else the
+    process built, and nothing outside this generation is touched (the IR module's own counter is
+    left alone)."""
+
+    def __init__(self, prog: ir.Program):
+        self.next = program_max_id(prog) + 1
+
+    def take(self) -> int:
+        self.next += 1
+        return self.next - 1
+
+
+def program_max_id(prog: ir.Program) -> int:
+    """The largest id of any buffer, kernel or loop variable of the program."""
+    top = max([0] + [b.id for b in prog.buffers] + [b.root.id for b in prog.buffers])
+    for k in ir.all_kernels(prog):
+        top = max(top, k.id, *[v.id for v in k.domain], *([v.id for v in k.red.vars] if k.red else []))
+    return top
+
+
+def new_var(ident: int, name: str, extent: int) -> Var:
+    """A loop variable with a chosen id (built with the IR's own constructor, then renumbered)."""
+    v = Var(name, extent)
+    v.id = ident
+    return v
+
+
+def new_buffer(ident: int, name: str, shape, dtype: str, kind: str) -> Buffer:
+    """A buffer of the backend's own (scratch, host-scalar copies) with a fixed id."""
+    b = Buffer(name, shape, dtype, kind)
+    b.id = ident
+    return b
+
+
 def rt_args(st, table) -> list:
     out = []
     for key in table.get(st.name, ()):

@@ -110,7 +110,7 @@ def im2col_copy(st):
     return k, store.buf.root, store.value, loads[0]
 
 
-def rewrite(c: ir.Kernel, cp):
+def rewrite(c: ir.Kernel, cp, ids):
     """c reading the copy's source in place of patches, or None (c is left as it is)."""
     from . import hip_gemm
     pk, dst, value, src = cp
@@ -144,7 +144,7 @@ def rewrite(c: ir.Kernel, cp):
         if len(run) == 1:
             pmap[run[0]] = ir.Affine.of(t)
         else:
-            parts = [Var(v.name, v.extent) for v in run]
+            parts = [A.new_var(ids.take(), v.name, v.extent) for v in run]
             splits[t] = parts
             for v, p in zip(run, parts):
                 pmap[v] = ir.Affine.of(p)
@@ -163,7 +163,7 @@ def rewrite(c: ir.Kernel, cp):
     return c3
 
 
-def forward_im2col_copies(prog: ir.Program) -> ir.Program:
+def forward_im2col_copies(prog: ir.Program, ids) -> ir.Program:
     """Each product that reads an im2col copy's output reads the copy's source instead (see the
     module docstring), when every reader of the copy's output can, and the copy is dropped. (One
     product left reading patches keeps the copy, and then the products over patches, with one
@@ -190,7 +190,7 @@ def forward_im2col_copies(prog: ir.Program) -> ir.Program:
                     break
                 c = s2.kernel
                 if dst.id in {x.id for x in A.kernel_reads(c)}:
-                    k2 = rewrite(c, cp)
+                    k2 = rewrite(c, cp, ids)
                     if k2 is None:
                         break
                     new[j] = dataclasses.replace(s2, kernel=k2)
@@ -344,7 +344,7 @@ def match_dgrad(gen, stmts: list, i: int):
         if solved is None:
             tvars.append((members[0], c))
             continue
-        y = Var(f"{solved.name}+", ext)
+        y = A.new_var(gen.ids.take(), f"{solved.name}+", ext)
         tvars.append((y, c))
         rmap[solved] = ir.Affine.of(y) - sum((ir.Affine.of(m) for m in members if m is not solved), ir.Affine(0))
         preds.append((solved, y, [m for m in members if m is not solved]))

@@ -743,8 +743,8 @@ class GemmPlan(Plan):
         """The partial tiles of a K split across workgroups: [slice][batch][M][N] floats."""
         if not hasattr(self, "_ws"):
             s = self.s
-            self._ws = ir.Buffer(f"{self.name}.partials", (self.kslices * s.B * s.M * s.N,), F32, "scratch",
-                                 id=800_000_000 + self.k.id)
+            self._ws = A.new_buffer(800_000_000 + self.k.id, f"{self.name}.partials",
+                                    (self.kslices * s.B * s.M * s.N,), F32, "scratch")
         return self._ws
 
     def epilogue(self, sc, loop, slot, value, hoisted, per):

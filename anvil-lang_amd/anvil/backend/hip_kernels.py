@@ -414,7 +414,7 @@ class GatherSumPlan(Plan):
         sc.stream_name = self.stream_param(k)
         body: list[str] = []
         em = Emitter(sc, body, "        ")
-        ys = [ir.Var(f"y{i}", t[1], id=900_000_000 + i) for i, t in enumerate(self.targets)]
+        ys = [A.new_var(900_000_000 + i, f"y{i}", t[1]) for i, t in enumerate(self.targets)]
         for line in decode(ys, "w", it):
             em.emit(line)
         for y, (_, _, members, solved) in zip(ys, self.targets):
@@ -1685,8 +1685,8 @@ class SlicePlan(Plan):
     def ws_buffer(self):
         """The partials, [slice][output]."""
         if not hasattr(self, "_ws"):
-            self._ws = ir.Buffer(f"{self.name}.partials", (self.kslices * self.R,), self.k.red.body.dtype,
-                                 "scratch", id=810_000_000 + self.k.id)
+            self._ws = A.new_buffer(810_000_000 + self.k.id, f"{self.name}.partials", (self.kslices * self.R,),
+                                    self.k.red.body.dtype, "scratch")
         return self._ws
 
     def second(self):

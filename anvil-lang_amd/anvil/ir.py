@@ -38,15 +38,6 @@ def bump_ids(at_least: int) -> None:
     _next_id = itertools.count(max(cur, at_least + 1))
 
 
-def restart_ids(after: int) -> int:
-    """Make the next fresh id after + 1, whatever was allocated before; returns the id that would
-    have come next (give it back to bump_ids to keep ids unique across programs afterwards)."""
-    global _next_id
-    cur = next(_next_id)
-    _next_id = itertools.count(after + 1)
-    return cur
-
-
 def prod(xs) -> int:
     out = 1
     for x in xs:
@@ -68,8 +59,8 @@ class Buffer:
     """A statically shaped f32/i32 array. `kind` is one of param state data temp var const grad
     scalar input output. `storage` points at the buffer whose memory this one reuses."""
 
-    def __init__(self, name, shape, dtype=F32, kind="temp", init=None, span=None, id=None):
-        self.id = fresh_id() if id is None else int(id)
+    def __init__(self, name, shape, dtype=F32, kind="temp", init=None, span=None):
+        self.id = fresh_id()
         self.name = name
         self.shape = tuple(int(d) for d in shape)
         self.dims = tuple(shape)
@@ -105,8 +96,8 @@ class Buffer:
 class Var:
     """A loop variable with a static extent."""
 
-    def __init__(self, name, extent=None, id=None):
-        self.id = fresh_id() if id is None else int(id)
+    def __init__(self, name, extent=None):
+        self.id = fresh_id()
         self.name = name
         self.dim = None
         self.extent = None if extent is None else int(extent)

@@ -243,7 +243,8 @@ def load(data) -> "ir.Program":
         init = bd["init"]
         if init is not None and bd["dtype"] == "f32":
             init = [_fnum(v) for v in init]
-        b = ir.Buffer(bd["name"], bd["shape"], bd["dtype"], bd["kind"], init=init, id=bd["id"])
+        b = ir.Buffer(bd["name"], bd["shape"], bd["dtype"], bd["kind"], init=init)
+        b.id = bd["id"]                                 # the ids the front end gave them
         if bd.get("heap"):
             b.heap = True
         bufs[b.id] = b
@@ -256,7 +257,8 @@ def load(data) -> "ir.Program":
         nonlocal max_id
         v = vars_.get(vd["id"])
         if v is None:
-            v = vars_[vd["id"]] = ir.Var(vd["name"], vd["extent"], id=vd["id"])
+            v = vars_[vd["id"]] = ir.Var(vd["name"], vd["extent"])
+            v.id = vd["id"]
             max_id = max(max_id, v.id)
         return v
 
@@ -369,8 +371,7 @@ def load(data) -> "ir.Program":
     main = block(data["main"])
     prog = ir.Program(main, [bufs[i] for i in sorted(bufs)],
                       None if data.get("source") is None else _Source(data["source"]))
-    ir.bump_ids(max_id)
-    prog.max_id = max_id                # the largest id the program holds (see hip.generate)
+    ir.bump_ids(max_id)                 # ids made later in this process do not collide with these
     return prog
 
 

@@ -151,13 +151,17 @@ def copy_program():
     """An IR program whose loop is one plain copy kernel B[i] = A[i] of COPY_ELEMS floats: the
     known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters into bytes."""
     from anvil import ir
-    a = ir.Buffer("A", (COPY_ELEMS,), "f32", "param", id=1)           # fixed ids: the same source,
-    b = ir.Buffer("B", (COPY_ELEMS,), "f32", "param", id=2)           # so the same built library,
-    i, j = ir.Var("i", COPY_ELEMS, id=3), ir.Var("j", COPY_ELEMS, id=4)  # in every process
+
+    def numbered(obj, ident):          # fixed ids: the same source, so the same built library,
+        obj.id = ident                 # in every process
+        return obj
+    a = numbered(ir.Buffer("A", (COPY_ELEMS,), "f32", "param"), 1)
+    b = numbered(ir.Buffer("B", (COPY_ELEMS,), "f32", "param"), 2)
+    i, j = numbered(ir.Var("i", COPY_ELEMS), 3), numbered(ir.Var("j", COPY_ELEMS), 4)
     fill = ir.Kernel([i], [ir.Store(a, ir.Affine(0, {i: 1}), ir.Rand(0))], name="fill", label="uniform", id=5)
     copy = ir.Kernel([j], [ir.Store(b, ir.Affine(0, {j: 1}), ir.Load(a, ir.Affine(0, {j: 1})))], name="copy",
                      label="copy", id=6)
-    it = ir.Buffer("it", (), "i32", "var", id=7)
+    it = numbered(ir.Buffer("it", (), "i32", "var"), 7)
     main = ir.Block([ir.KernelStmt(fill), ir.For(it, 0, COPY_LAUNCHES, 1, ir.Block([ir.KernelStmt(copy)]))])
     return ir.Program(main, [a, b, it])
 

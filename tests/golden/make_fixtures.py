@@ -2,7 +2,9 @@
 
 Run in the development container only (the reference checkout is not on the GPU box):
 
-    python tests/golden/make_fixtures.py [/root/reference]
+    python tests/golden/make_fixtures.py [/root/reference] [NAME ...] [--route-only]
+
+(--route-only: the IR and the reference-route source hashes, without running the interpreter.)
 
 For each program in `programs.py` (Anvil source written for this repository's tests and
 workloads) it writes:
@@ -17,6 +19,7 @@ NPZ files. The reference's own code is imported only by this script.
 """
 from __future__ import annotations
 
+import hashlib
 import importlib.util
 import io
 import json
@@ -39,6 +42,22 @@ def _irjson():
     return mod
 
 
+def _backend_on_reference():
+    """This repository's HIP backend modules loaded as members of the reference's own
+    `anvil.backend` package, so that their `from .. import ir` is the reference's ir module and
+    `generate` receives the reference's own Program objects (the drop-in route)."""
+    import anvil.backend as ref_backend
+    ours = os.path.join(REPO, "anvil-lang_amd", "anvil", "backend")
+    if ours not in ref_backend.__path__:
+        ref_backend.__path__.append(ours)
+    import anvil.backend.hip as hip
+    assert hip.ir.__file__.startswith(os.path.dirname(ref_backend.__file__).rsplit(os.sep, 1)[0])
+    return hip
+
+
+ROUTE = os.path.join(HERE, "reference_route.json")
+
+
 def main(ref_root: str) -> None:
     sys.path.insert(0, ref_root)
     from anvil.driver import compile_text          # the reference front end
@@ -48,9 +67,16 @@ def main(ref_root: str) -> None:
     import programs
 
     irjson = _irjson()
+    hip = _backend_on_reference()
     os.makedirs(os.path.join(HERE, "ir"), exist_ok=True)
     os.makedirs(os.path.join(HERE, "vectors"), exist_ok=True)
-    only = set(sys.argv[2:])
+    args = sys.argv[2:]
+    route_only = "--route-only" in args
+    only = set(a for a in args if not a.startswith("--"))
+    route = {}
+    if os.path.exists(ROUTE):
+        with open(ROUTE) as f:
+            route = json.load(f)
     for spec in programs.PROGRAMS:
         name = spec["name"]
         if only and name not in only:
@@ -79,11 +105,17 @@ def main(ref_root: str) -> None:
         data["seed"] = spec.get("seed", 0)
         if spec.get("check"):
             data["check"] = spec["check"]                # built and run with --check=<mode>
+        # the source the backend generates from the reference's own objects (sha256): the JSON
+        # route must give the same bytes (tests/test_reference_route.py)
+        src = hip.generate(prog, seed=data["seed"], library=bool(spec.get("function")), graphs=False,
+                           check=spec.get("check"))
+        route[name] = {"sha256": hashlib.sha256(src.encode()).hexdigest(), "library": bool(spec.get("function")),
+                       "bytes": len(src)}
         with open(os.path.join(HERE, "ir", f"{name}.json"), "w") as f:
             json.dump(data, f, separators=(",", ":"))
         nk = sum(1 for _ in _kernels(data["main"]))
-        print(f"{name}: {nk} kernels", flush=True)
-        if not spec.get("interp"):
+        print(f"{name}: {nk} kernels, source {route[name]['sha256'][:12]}", flush=True)
+        if not spec.get("interp") or route_only:
             continue
         out = io.StringIO()
         it = Interpreter(prog, out=out, seed=spec.get("seed", 0), inp=io.StringIO(spec.get("stdin", "")),
@@ -115,6 +147,8 @@ def main(ref_root: str) -> None:
                     arrays[f"output{k}"] = it.arr(b)[:b.numel].reshape(b.shape).copy()
         arrays["stdout"] = np.frombuffer(out.getvalue().encode(), dtype=np.uint8)
         np.savez_compressed(os.path.join(HERE, "vectors", f"{name}.npz"), **arrays)
+    with open(ROUTE, "w") as f:
+        json.dump(dict(sorted(route.items())), f, indent=1)
 
 
 def _kernels(stmts):

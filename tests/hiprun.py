@@ -6,8 +6,11 @@ run in this process through the library-mode ABI (anvil.hip_function.Compiled).
 
 Comparison rules (the bar the backend is held to):
   - printed text must be identical apart from numbers;
-  - integers (and so shuffled permutations, gathered indices, argmax results) bit for bit;
-  - a printed float within `rtol` of the reference's, or within one unit of its last printed digit;
+  - integers (and so shuffled permutations, gathered indices, argmax results, counts, device-drawn
+    randint values) bit for bit: a token printed without a point or exponent must be the same text;
+  - a printed float within `rtol` of the reference's, or within one unit of its last printed digit,
+    and printed the same way (same decimals, same fixed or scientific notation, except for two
+    values that straddle the default format's switch at 1e6 or 1e-4);
   - a float tensor within `rtol` of the reference's, relative to the tensor's largest magnitude.
 """
 from __future__ import annotations
@@ -56,6 +59,34 @@ def _unit(token: str) -> float:
     return 10.0 ** (-dec) * (10.0 ** int(exp) if exp else 1.0)
 
 
+def _is_integer(token: str) -> bool:
+    """A printed integer: digits with an optional sign, no point, no exponent (`%d`, i32 tensors)."""
+    return token.lstrip("+-").isdigit()
+
+
+def _form(token: str) -> tuple:
+    """How a float was printed: decimals after the point, and fixed (%.Nf) or scientific (%.Ne)."""
+    mant, e, _ = token.lower().partition("e")
+    return (len(mant.split(".")[1]) if "." in mant else 0, bool(e))
+
+
+def number_mismatch(x: str, y: str, rtol: float) -> bool:
+    """True if the printed number y does not stand for the reference's x under the rules above."""
+    if x == y:
+        return False
+    if _is_integer(x) or _is_integer(y):
+        return True                                    # integers (and argmax, counts) bit for bit
+    fx, fy = float(x), float(y)
+    if np.isnan(fx) and np.isnan(fy):
+        return False
+    if _form(x) != _form(y):
+        # the default format switches between %.4f and %.4e at |v| = 1e6 and 1e-4: two values
+        # within rtol of each other may straddle that line, and nothing else changes the form
+        near = any(abs(abs(fx) - edge) <= rtol * edge for edge in (1e6, 1e-4))
+        return not (near and abs(fx - fy) <= rtol * abs(fx))
+    return abs(fx - fy) > max(rtol * abs(fx), 1.01 * _unit(x))
+
+
 def outputs_match(want: str, got: str, rtol: float) -> str | None:
     """None if the texts match under the rules above, else a description of the first difference."""
     wl, gl = want.splitlines(), got.splitlines()
@@ -69,13 +100,15 @@ def outputs_match(want: str, got: str, rtol: float) -> str | None:
         if ta != tb or len(na) != len(nb):
             return f"line {i + 1}: {b!r}, expected {a!r}"
         for x, y in zip(na, nb):
-            fx, fy = float(x), float(y)
-            if x == y or (np.isnan(fx) and np.isnan(fy)):
-                continue
-            if abs(fx - fy) <= max(rtol * abs(fx), 1.01 * _unit(x)):
-                continue
-            return f"line {i + 1}: {y} where the reference printed {x} ({b!r})"
+            if number_mismatch(x, y, rtol):
+                return f"line {i + 1}: {y} where the reference printed {x} ({b!r})"
     return None
+
+
+def accuracy_tokens(text: str) -> list[str]:
+    """The printed test accuracies (`accuracy X`): a count of argmax hits over the test set divided
+    by its size, so it must be the same text as the reference's, not merely close."""
+    return re.findall(r"accuracy\s+(\S+)", text)
 
 
 def tensors_match(want: np.ndarray, got: np.ndarray, rtol: float) -> str | None:

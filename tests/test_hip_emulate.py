@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from fixtures import stdout_of, vectors
-from hiprun import function_call, kept_buffers, outputs_match, patched_program, run_program, tensors_match
+from hiprun import accuracy_tokens, function_call, kept_buffers, outputs_match, patched_program, run_program, tensors_match
 
 PROGRAMS = ["hello", "linreg", "attention_train", "split", "scatter", "integers", "formats", "control",
             "products", "c1_small", "c2_small", "c2_steps100", "mnist_like", "c4_small", "c4_mid", "c5_small", "c5_mid"]
@@ -29,6 +29,7 @@ def test_program_matches_reference(name):
     z = vectors(name)
     problem = outputs_match(stdout_of(z), out, rtol=1e-3 if name in TRAINED else 1e-4)
     assert problem is None, problem
+    assert accuracy_tokens(out) == accuracy_tokens(stdout_of(z)), "test accuracy differs"
     for k in keep:
         problem = tensors_match(z[f"buf:{k}"], arrays[k], rtol=1e-3)
         assert problem is None, f"{k}: {problem}"

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from fixtures import load_ir, stdout_of, vectors
-from hiprun import function_call, kept_buffers, outputs_match, patched_program, run_program, tensors_match
+from hiprun import accuracy_tokens, function_call, kept_buffers, outputs_match, patched_program, run_program, tensors_match
 from test_hip_emulate import FUNCTIONS, PROGRAMS, TRAINED
 
 pytestmark = pytest.mark.gpu
@@ -25,6 +25,7 @@ def test_gpu_program_matches_reference(name):
     z = vectors(name)
     problem = outputs_match(stdout_of(z), out, rtol=1e-3 if name in TRAINED else 1e-4)
     assert problem is None, problem
+    assert accuracy_tokens(out) == accuracy_tokens(stdout_of(z)), "test accuracy differs"
     for k in keep:
         problem = tensors_match(z[f"buf:{k}"], arrays[k], rtol=1e-3)
         assert problem is None, f"{k}: {problem}"
@@ -61,6 +62,7 @@ def test_gpu_full_size_program_matches_reference(name):
     z = vectors(name)
     problem = outputs_match(stdout_of(z), out, rtol=2e-3 if name == "c2_full" else 1e-3)
     assert problem is None, problem
+    assert accuracy_tokens(out) == accuracy_tokens(stdout_of(z)), "test accuracy differs"
     for k in keep:
         ref, got = z[f"buf:{k}"].astype(np.float64), arrays[k].astype(np.float64)
         if name == "c5_full3":

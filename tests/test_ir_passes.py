@@ -28,7 +28,7 @@ def test_implicit_convolution_rewrite_keeps_the_program():
     """c5_mid: both products over the second convolution's im2col copy read the copy's source
     through the window (their merged variables split back out), and the copy is dropped."""
     prog, data = load_ir("c5_mid")
-    new = hip_conv.forward_im2col_copies(prog)
+    new = hip_conv.forward_im2col_copies(prog, A.IdSource(prog))
     before, after = kernels(prog), kernels(new)
     assert len(after) == len(before) - 1                          # the im2col copy of conv2 is gone
     split = [k for k in after if k not in before and k.red is not None]
