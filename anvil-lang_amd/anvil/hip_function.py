@@ -9,7 +9,7 @@ each call points the `anvil_input<k>` / `anvil_output<k>` slots at the caller's 
 
 NumPy arguments live in host memory, so each call copies them to the device and the results back
 (the slots hold host pointers, exactly as in the reference's ABI). `call_device` is the extension
-for arrays that already live on the GPU (ROCm torch tensors, or anything with a device pointer): the
+for arrays that already live on the GPU (ROCm torch tensors, or `DeviceArray`s): the
 same program reads and writes them in place through the `anvil_dinput<k>` / `anvil_doutput<k>`
 slots, with no copies.
 
@@ -106,7 +106,9 @@ class Compiled:
         return self._result(results)
 
     def call_device(self, tensors, outputs=None):
-        """Device arrays in and out: objects with .data_ptr() (torch) or integer device addresses.
+        """Device arrays in and out: ROCm torch tensors, or DeviceArray (below). Each must have the
+        shape and dtype the function was compiled for and be contiguous on the GPU; anything else is
+        refused before the library sees its address (the kernels would read or write past it).
         `outputs` are preallocated device arrays for the results (torch tensors are made if None)."""
         self._check(tensors)
         if outputs is None:
@@ -115,16 +117,17 @@ class Compiled:
             outputs = [None if b is None else torch.empty(b.shape, device=dev,
                                                           dtype=torch.float32 if b.dtype == "f32" else torch.int32)
                        for b in self.outputs]
-
-        def ptr(t):
-            return t if isinstance(t, int) else t.data_ptr()
+        if len(outputs) != len(self.outputs):
+            raise TypeError(f"{self.name} has {len(self.outputs)} results, got {len(outputs)} output arrays")
+        in_ptrs = [device_pointer(t, b) for t, b in zip(tensors, self.inputs)]
+        out_ptrs = [None if b is None else device_pointer(t, b) for t, b in zip(outputs, self.outputs)]
         with self.lock:
-            for slot, t in zip(self.din_slots, tensors):
+            for slot, p in zip(self.din_slots, in_ptrs):
                 if slot is not None:
-                    slot.value = ptr(t)
-            for slot, t in zip(self.dout_slots, outputs):
+                    slot.value = p
+            for slot, p in zip(self.dout_slots, out_ptrs):
                 if slot is not None:
-                    slot.value = ptr(t)
+                    slot.value = p
             self.lib.lib.anvil_entry_device()
             for slot in self.din_slots + self.dout_slots:
                 if slot is not None:
@@ -135,3 +138,73 @@ class Compiled:
         consts = iter(self.consts)
         out = [next(consts) if r is None else (r[()] if getattr(r, "ndim", 1) == 0 else r) for r in results]
         return tuple(out) if self.tuple_result else out[0]
+
+
+def device_pointer(t, b) -> int:
+    """The device address of t, after checking that t can stand for buffer b: same shape and dtype,
+    contiguous, on the GPU, 16-byte aligned (the kernels load 16 bytes at a time)."""
+    want = "float32" if b.dtype == "f32" else "int32"
+    if hasattr(t, "is_cuda"):                                           # a torch tensor
+        if not t.is_cuda:
+            raise ValueError(f"{b.name}: a device array is needed, got a tensor on {t.device}")
+        if str(t.dtype) != f"torch.{want}":
+            raise TypeError(f"{b.name}: dtype {t.dtype}, compiled for {want}")
+        if tuple(t.shape) != tuple(b.shape):
+            raise ValueError(f"{b.name}: shape {tuple(t.shape)}, compiled for {tuple(b.shape)}")
+        if not t.is_contiguous():
+            raise ValueError(f"{b.name}: the tensor is not contiguous")
+        p = t.data_ptr()
+    elif isinstance(t, DeviceArray):
+        if t.dtype != want or tuple(t.shape) != tuple(b.shape):
+            raise ValueError(f"{b.name}: {t.dtype}{list(t.shape)}, compiled for {want}{list(b.shape)}")
+        p = t.data_ptr()
+    else:
+        raise TypeError(f"{b.name}: expected a torch tensor on the GPU or a DeviceArray, got {type(t).__name__}")
+    if p % 16:
+        raise ValueError(f"{b.name}: device address {p:#x} is not 16-byte aligned")
+    return p
+
+
+class DeviceArray:
+    """A contiguous f32/i32 array in device memory, allocated through the HIP runtime itself (no
+    framework needed): for callers that keep their data on the GPU between calls."""
+
+    _hip = None
+
+    def __init__(self, shape, dtype="float32"):
+        if DeviceArray._hip is None:
+            DeviceArray._hip = ctypes.CDLL("libamdhip64.so")
+        self.shape = tuple(int(d) for d in shape)
+        self.dtype = np.dtype(dtype).name
+        if self.dtype not in ("float32", "int32"):
+            raise TypeError(f"DeviceArray holds float32 or int32, not {self.dtype}")
+        self.nbytes = 4 * int(np.prod(self.shape, dtype=np.int64))
+        self.ptr = ctypes.c_void_p()
+        rc = DeviceArray._hip.hipMalloc(ctypes.byref(self.ptr), ctypes.c_size_t(max(self.nbytes, 16)))
+        if rc != 0:
+            raise MemoryError(f"hipMalloc of {self.nbytes} bytes failed (status {rc})")
+
+    @classmethod
+    def from_host(cls, a) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        d._copy(d.ptr, a.ctypes.data_as(ctypes.c_void_p), 1)
+        return d
+
+    def to_host(self):
+        a = np.empty(self.shape, self.dtype)
+        self._copy(a.ctypes.data_as(ctypes.c_void_p), self.ptr, 2)
+        return a
+
+    def _copy(self, dst, src, kind):
+        rc = DeviceArray._hip.hipMemcpy(dst, src, ctypes.c_size_t(self.nbytes), kind)
+        if rc != 0:
+            raise RuntimeError(f"hipMemcpy failed (status {rc})")
+
+    def data_ptr(self) -> int:
+        return self.ptr.value
+
+    def free(self):
+        if self.ptr.value:
+            DeviceArray._hip.hipFree(self.ptr)
+            self.ptr = ctypes.c_void_p()

@@ -184,31 +184,12 @@ def copy_run() -> dict:
 C3 = ["c3_softmax", "c3_layernorm", "c3_linear", "c3_attention"]
 
 
-class DeviceArray:
-    """A device allocation through the HIP runtime itself (no framework needed): inputs are
-    resident in HBM before the timed calls, as the metric asks."""
-
-    hip = None
-
-    def __init__(self, host):
-        if DeviceArray.hip is None:
-            DeviceArray.hip = ctypes.CDLL("libamdhip64.so")
-        self.nbytes = host.nbytes
-        self.ptr = ctypes.c_void_p()
-        if DeviceArray.hip.hipMalloc(ctypes.byref(self.ptr), ctypes.c_size_t(max(self.nbytes, 4))) != 0:
-            raise SystemExit("bench: hipMalloc failed")
-        DeviceArray.hip.hipMemcpy(self.ptr, host.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(self.nbytes), 1)
-
-    def data_ptr(self):
-        return self.ptr.value
-
-
 def c3_run(calls: int) -> dict:
     """Config C3: each anvil.function at its BASELINE size, inputs ~N(0,1) (seed 2) already on the
     device; every generated kernel timed with dispatch events over `calls` calls."""
     import numpy as np
     from anvil import irjson
-    from anvil.hip_function import Compiled, Lowered
+    from anvil.hip_function import Compiled, DeviceArray, Lowered
     out = {}
     for name in C3:
         with open(os.path.join(ROOT, "tests", "golden", "ir", f"{name}.json")) as f:
@@ -217,13 +198,13 @@ def c3_run(calls: int) -> dict:
         low = Lowered.from_fixture(prog, data)
         fn = Compiled(name, low, seed=int(data.get("seed", 0)))
         rng = np.random.default_rng(2)
-        args = [DeviceArray(rng.standard_normal(b.shape).astype(np.float32)) for b in low.inputs]
-        res = [DeviceArray(np.zeros(b.shape, np.float32)) for b in low.outputs]
-        fn.call_device([a.data_ptr() for a in args], [r.data_ptr() for r in res])      # warm-up
+        args = [DeviceArray.from_host(rng.standard_normal(b.shape).astype(np.float32)) for b in low.inputs]
+        res = [DeviceArray(b.shape) for b in low.outputs]
+        fn.call_device(args, res)                                                          # warm-up
         fn.lib.lib.anvil_profile_enable(1)
         fn.lib.lib.anvil_profile_reset()
         for _ in range(calls):
-            fn.call_device([a.data_ptr() for a in args], [r.data_ptr() for r in res])
+            fn.call_device(args, res)
         kernels = []
         for label, ms, n, flops, nbytes in fn.lib.profile():
             if n == 0:

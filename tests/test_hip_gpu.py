@@ -9,6 +9,7 @@ by __graft_entry__.build() (they are looked up by the hash of their source).
 import numpy as np
 import pytest
 
+import closed_forms
 from fixtures import load_ir, stdout_of, vectors
 from hiprun import accuracy_tokens, function_call, kept_buffers, outputs_match, patched_program, run_program, tensors_match
 from test_hip_emulate import FUNCTIONS, PROGRAMS, TRAINED
@@ -91,16 +92,10 @@ def test_gpu_attention_at_full_size_matches_closed_form():
     """C3's attention, Q, K, V [4, 2048, 128]: the one-kernel path (scores never stored) against
     softmax(Q Kᵀ / √128) V computed in float64."""
     print("gpu attention full size", flush=True)
-    from anvil.hip_function import Compiled, Lowered
     prog, data = load_ir("c3_attention")
     assert any("attention:" in line for line in _source_lines(prog, data)), "not the one-kernel schedule"
-    low = Lowered.from_fixture(prog, data)
-    rng = np.random.default_rng(2)
-    q, k, v = (rng.standard_normal((4, 2048, 128)).astype(np.float32) for _ in range(3))
-    got = Compiled(low.name, low, seed=data.get("seed", 0)).call([q, k, v])
-    s = np.einsum("bid,bjd->bij", q.astype(np.float64), k.astype(np.float64)) / np.sqrt(128.0)
-    p = np.exp(s - s.max(axis=2, keepdims=True))
-    want = np.einsum("bij,bjd->bid", p / p.sum(axis=2, keepdims=True), v.astype(np.float64))
+    args, want = closed_forms.attention_case()
+    got = _full_size_call("c3_attention", args)
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
 
 
@@ -116,10 +111,8 @@ def test_gpu_softmax_at_full_size_matches_closed_form():
     """C3's softmax over the rows of [8192, 4096] (inputs ~N(0,1), seed 2) against float64 NumPy;
     every row also sums to 1."""
     print("gpu softmax full size", flush=True)
-    x = np.random.default_rng(2).standard_normal((8192, 4096)).astype(np.float32)
-    got = _full_size_call("c3_softmax", [x])
-    e = np.exp(x.astype(np.float64) - x.max(axis=1, keepdims=True))
-    want = e / e.sum(axis=1, keepdims=True)
+    args, want = closed_forms.softmax_case()
+    got = _full_size_call("c3_softmax", args)
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-7)
     np.testing.assert_allclose(got.astype(np.float64).sum(axis=1), 1.0, rtol=0, atol=1e-4)
 
@@ -127,30 +120,19 @@ def test_gpu_softmax_at_full_size_matches_closed_form():
 def test_gpu_layernorm_at_full_size_matches_closed_form():
     """C3's layer_norm(x)·γ + β at [8192, 1024] (eps 1e-5, biased variance) against float64 NumPy."""
     print("gpu layernorm full size", flush=True)
-    rng = np.random.default_rng(2)
-    x = rng.standard_normal((8192, 1024)).astype(np.float32)
-    g = rng.standard_normal(1024).astype(np.float32)
-    b = rng.standard_normal(1024).astype(np.float32)
-    got = _full_size_call("c3_layernorm", [x, g, b])
-    x64 = x.astype(np.float64)
-    mu = x64.mean(axis=1, keepdims=True)
-    var = ((x64 - mu) ** 2).mean(axis=1, keepdims=True)
-    want = (x64 - mu) / np.sqrt(var + 1e-5) * g + b
+    args, want = closed_forms.layernorm_case()
+    got = _full_size_call("c3_layernorm", args)
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4)
 
 
 def test_gpu_linear_at_full_size_matches_closed_form():
-    """C3's linear y = x·Wᵀ + b at [8192, 4096] × [4096, 4096] (the 128 x 128 tile schedule): one row
-    of each of the 64 row tiles, at a different place in each tile, against float64 NumPy."""
+    """C3's linear y = x·Wᵀ + b at [8192, 4096] × [4096, 4096]: one row of each of the 64 row tiles
+    of 128 rows, at a different place in each tile, against float64 NumPy."""
     print("gpu linear full size", flush=True)
-    rng = np.random.default_rng(2)
-    x = rng.standard_normal((8192, 4096)).astype(np.float32)
-    w = rng.standard_normal((4096, 4096)).astype(np.float32)
-    b = rng.standard_normal(4096).astype(np.float32)
-    got = _full_size_call("c3_linear", [x, w, b])
-    rows = 128 * np.arange(64) + (37 * np.arange(64)) % 128
-    want = x[rows].astype(np.float64) @ w.astype(np.float64).T + b
-    np.testing.assert_allclose(got[rows], want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
+    args, want = closed_forms.linear_case()
+    got = _full_size_call("c3_linear", args)
+    np.testing.assert_allclose(got[closed_forms.LINEAR_ROWS], want, rtol=1e-4,
+                               atol=1e-5 * float(np.max(np.abs(want))))
 
 
 def test_gpu_linear_2x2_tiles_matches_closed_form():
