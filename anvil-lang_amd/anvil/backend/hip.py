@@ -876,8 +876,13 @@ class HipGen:
         self.device_bufs[HSD_ID] = A.new_buffer(HSD_ID, "host_scalars.device_copy", (max(1, len(self.hsd)),), I32,
                                                 "scratch")
         dev = sorted(self.device_bufs.values(), key=lambda b: b.id)
-        plan = A.plan_arena(self.prog, dev, self.full_writer, share=os.environ.get("ANVIL_HIP_SHARE", "1") != "0",
-                            fused=self.fused_group)
+        share = os.environ.get("ANVIL_HIP_SHARE", "1") != "0"
+        plan = A.plan_arena(self.prog, dev, self.full_writer, share=share, fused=self.fused_group)
+        # the no-allocation entry: the caller brings the arguments and results, so its scratch
+        # holds only the other buffers (same lifetime sharing)
+        extern_ids = {b.id for b in externs}
+        inner = [b for b in dev if b.id not in extern_ids]
+        splan = A.plan_arena(self.prog, inner, self.full_writer, share=share, fused=self.fused_group)
         src = self.prog.source
         name = src.display_path() if src is not None and hasattr(src, "display_path") else "<program>"
         out = [f"// Generated by anvil (HIP backend) from {name} for MI355X ({ARCH}).",
@@ -896,6 +901,11 @@ class HipGen:
                    ", ".join(f"[{i}] {self.by_id[bid].name}" for bid, i in sorted(self.hsd.items(), key=lambda t: t[1])))
         for n in range(len(self.segments)):
             out.append(f"static anvil_segment anvil_seg{n};")
+        need = splan.size if inner else 0
+        out += ["// scratch of anvil_entry_noalloc: every buffer but the arguments and results, at the",
+                "// offsets of the same lifetime plan; one copy per GPU, held until the process ends",
+                f"static const long long anvil_scratch_need = {need}LL;",
+                f"ANVIL_SCRATCH_ARRAY(anvil_scratch, {need if 0 < need <= SCRATCH_MAX else 256});"]
         for b in self.prog.buffers:
             r = b.root
             if r is b and r.init is not None:
@@ -912,19 +922,26 @@ class HipGen:
         sites = sites or ['{"none", 0.0, 0, 0.0, 0.0}']
         out.append(f"static anvil_site anvil_site_table[] = {{{', '.join(sites)}}};")
         out += ["", "// ---------------------------------------------------------------- set-up"]
+        out.append("// what the host needs, whichever entry runs first (allocates nothing)")
+        out.append("static void anvil_setup_host(void) {")
+        out.append("    static int done = 0;")
+        out.append("    if (done) return;")
+        out.append("    done = 1;")
+        for i, m in enumerate(self.faults, 1):
+            out.append(f"    anvil_fault_text[{i}] = {c_string(m)};")
+        out.append("    anvil_sites = anvil_site_table;")
+        out.append(f"    anvil_nsites = {len(self.plans)};")
+        out.append(f"    anvil_hs.seed0 = {self.seed}u;")
+        out.append("}")
         out.append("static void anvil_setup(void) {")
         out.append("    if (anvil_dev.ready) return;")
+        out.append("    anvil_setup_host();")
         out.append(f"    anvil_device_open({plan.size});")
         for b in dev:
             out.append(f"    anvil_b{b.id} = ({ctype(b.dtype)} *)(anvil_dev.arena + {plan.offsets[b.id]});")
         out.append(f"    anvil_hsd = (uint32_t *)anvil_b{HSD_ID};")
         for b in sorted(self.mirrored.values(), key=lambda b: b.id):
             out.append(f"    anvil_mirror_init(&anvil_mir{b.id}, (void **)&anvil_b{b.id}, {max(4, 4 * b.numel)});")
-        for i, m in enumerate(self.faults, 1):
-            out.append(f"    anvil_fault_text[{i}] = {c_string(m)};")
-        out.append("    anvil_sites = anvil_site_table;")
-        out.append(f"    anvil_nsites = {len(self.plans)};")
-        out.append(f"    anvil_hs.seed0 = {self.seed}u;")
         out.append("}")
         out += ["", "// the state a run starts from: zeroed memory, constants uploaded, seed and stream reset",
                 "static void anvil_fresh(void) {",
@@ -965,7 +982,84 @@ class HipGen:
             out.append(line)
         out += ["    goto anvil_end;", "anvil_end:", "    anvil_sync();", "    fflush(stdout);", "    return 0;", "}"]
         out += self.abi(externs, plan)
+        out += self.abi_noalloc(externs, dev, splan, need, HSD_ID)
         return "\n".join(out) + "\n"
+
+    def abi_noalloc(self, externs, dev, splan, need, hsd_id) -> list[str]:
+        """anvil_entry_noalloc: one call of the function on the caller's device buffers and stream,
+        with every other buffer in the library's static `anvil_scratch` array; no allocation of any
+        kind (no hipMalloc, pinned host memory, events or graphs). Refused (a negative status and a
+        message on stderr, nothing run) when an argument's size differs from the compiled shape, when
+        the scratch would exceed SCRATCH_MAX, or when the program keeps host copies of device
+        buffers (prints, data files, checkpoints) or runs --check, which allocate."""
+        def slot(b):
+            return int(b.name[len(b.kind):]) if b.name[len(b.kind):].isdigit() else None
+        ins = [(slot(b), b) for b in externs if b.kind == "input"]
+        outs = [(slot(b), b) for b in externs if b.kind == "output"]
+        n_in = 1 + max([k for k, _ in ins if k is not None], default=-1)
+        n_out = 1 + max([k for k, _ in outs if k is not None], default=-1)
+        why = None
+        if any(k is None for k, _ in ins + outs):
+            why = "its arguments are not numbered input<k>/output<k> slots"
+        elif self.mirrored:
+            why = "the program keeps host copies of device buffers (prints, data files, checkpoints)"
+        elif self.check:
+            why = "it was built with --check"
+        extern_ids = {b.id for b in externs}
+        out = ["",
+               "// No allocation: the caller's device buffers and stream, the other buffers in anvil_scratch.",
+               "// Calls that overlap on one GPU share its anvil_scratch and race: serialize them.",
+               "static void anvil_bind_scratch(char *base) {"]
+        for b in dev:
+            if b.id not in extern_ids:
+                out.append(f"    anvil_b{b.id} = ({ctype(b.dtype)} *)(base + {splan.offsets[b.id]});")
+        out.append(f"    anvil_hsd = (uint32_t *)anvil_b{hsd_id};")
+        out += ["}", 'extern "C" {',
+                "int anvil_entry_noalloc(void *const *inputs, const long long *input_bytes, int n_inputs,",
+                "                        void *const *outputs, const long long *output_bytes, int n_outputs,",
+                "                        void *stream) {"]
+        if why is not None:
+            out += [f"    (void)inputs; (void)input_bytes; (void)n_inputs; (void)outputs; (void)output_bytes;",
+                    f"    (void)n_outputs; (void)stream;",
+                    f"    return anvil_refuse(-4, {c_string('this library cannot run without allocating: ' + why + '; use anvil_entry_device')});",
+                    "}", "}", ""]
+            return out
+        out += [f"    if (n_inputs != {n_in} || n_outputs != {n_out})",
+                f'        return anvil_refuse(-1, "takes {n_in} inputs and {n_out} outputs, got %d and %d", n_inputs, n_outputs);',
+                f"    if (anvil_scratch_need > ANVIL_SCRATCH_MAX)",
+                f'        return anvil_refuse(-3, "needs %lld bytes of scratch, more than its maximum of %lld (use anvil_entry_device)", anvil_scratch_need, ANVIL_SCRATCH_MAX);']
+        for side, arr, sizes, items in (("input", "inputs", "input_bytes", ins), ("output", "outputs", "output_bytes", outs)):
+            for k, b in sorted(items, key=lambda t: t[0]):
+                out.append(f"    if ({arr}[{k}] == NULL || {sizes}[{k}] != {4 * b.numel}LL)")
+                out.append(f'        return anvil_refuse(-2, "{side} {k} must be a device buffer of {4 * b.numel} bytes ({b.dtype}{list(b.shape)}), got %lld bytes at %p", {sizes}[{k}], {arr}[{k}]);')
+        out += ["    anvil_fault_t *fault = NULL;",
+                "    char *base = anvil_scratch_here(&fault);",
+                "    if (base == NULL) return anvil_refuse(-5, \"cannot find its scratch array on the current device\");",
+                "    anvil_setup_host();",
+                "    const anvil_device_state saved = anvil_dev;",
+                "    uint32_t *keep_hsd = anvil_hsd;"]
+        for b in dev:
+            out.append(f"    {ctype(b.dtype)} *keep{b.id} = anvil_b{b.id};")
+        out += ["    anvil_noalloc_begin(stream, fault);",
+                "    anvil_bind_scratch(base);"]
+        for k, b in ins:
+            out.append(f"    anvil_b{b.id} = ({ctype(b.dtype)} *)inputs[{k}];")
+        for k, b in outs:
+            out.append(f"    anvil_b{b.id} = ({ctype(b.dtype)} *)outputs[{k}];")
+        out += ["    anvil_zero_scratch(base, anvil_scratch_need);     // every call starts from zeroed scratch",
+                "    const int prof = anvil_prof.on, suspended = anvil_graphs.suspended;",
+                "    anvil_prof.on = 0;",
+                "    anvil_graphs.suspended = 1;",
+                "    anvil_hs.seed = anvil_hs.seed0; anvil_hs.stream = 0;",
+                "    const int rc = anvil_program();",
+                "    anvil_prof.on = prof;",
+                "    anvil_graphs.suspended = suspended;",
+                "    anvil_dev = saved;",
+                "    anvil_hsd = keep_hsd;"]
+        for b in dev:
+            out.append(f"    anvil_b{b.id} = keep{b.id};")
+        out += ["    return rc;", "}", "}", ""]
+        return out
 
     def fused_group(self, k):
         """(launch key, buffers k's own kernel writes) when k is one of several IR kernels of a launch."""
@@ -1073,6 +1167,9 @@ def generate(prog: ir.Program, seed: int = 0, library: bool = False, emulate: bo
     if check not in (None, "nan", "inf"):
         raise ValueError(f"check must be None, 'nan' or 'inf', not {check!r}")
     return HipGen(prog, seed=seed, library=library, emulate=emulate, graphs=graphs, check=check).generate()
+
+
+SCRATCH_MAX = 64 << 20      # bytes: the largest anvil_scratch a library holds (ANVIL_SCRATCH_MAX)
 
 
 def hipcc() -> str:

@@ -35,6 +35,23 @@ int anvil_entry(void);
  * ABI assumes host memory, pyapi.py:287-292): for callers whose data is already on the GPU. */
 int anvil_entry_device(void);
 
+/* One call of the lowered function that allocates nothing: no hipMalloc or hipFree, no pinned host
+ * memory, no events or graphs. No counterpart in the reference; it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * inputs[k] / outputs[k] are the device buffers of argument k and result k (input_bytes[k] /
+ * output_bytes[k] must equal their compiled sizes: shapes are fixed when a function is lowered);
+ * the work is queued on `stream` (a hipStream_t; NULL: the null stream) and the call returns after
+ * it finished. The function's other buffers live in the library's static device array
+ * `anvil_scratch`, one per GPU the library runs on, held until the process ends, at most
+ * ANVIL_SCRATCH_MAX = 64 MiB and cleared at the start of every call. Calls that overlap on one GPU
+ * share that array and race: serialize them. Returns 0, or, with a message on stderr and nothing
+ * run: -1 wrong number of arguments, -2 an argument of the wrong size, -3 the function needs more
+ * scratch than the maximum, -4 the library cannot run without allocating (it prints, reads data
+ * files, checkpoints or was built with --check), -5 the scratch array is not found on the current
+ * device. A run-time error of the program ends the process with status 1, as in anvil_entry. */
+int anvil_entry_noalloc(void *const *inputs, const long long *input_bytes, int n_inputs,
+                        void *const *outputs, const long long *output_bytes, int n_outputs, void *stream);
+
 /* Set the library up (device, arena, constants) without running anything. */
 int anvil_init(void);
 

@@ -482,6 +482,9 @@ PROGRAMS = [
      "function": {"name": "linear", "args": [([2048, 64], "f32"), ([128, 64], "f32"), ([128], "f32")]}},
     {"name": "c3_attention_small", "source": C3_ATTENTION, "interp": True,
      "function": {"name": "attention", "args": [([2, 64, 32], "f32")] * 3}},
+    # the same function at half the keys and head size: a second, smaller compilation
+    {"name": "c3_attention_tiny", "source": C3_ATTENTION, "interp": True,
+     "function": {"name": "attention", "args": [([2, 32, 16], "f32")] * 3}},
     # shapes the one-kernel attention takes (head size 64 and 128, keys a multiple of 128)
     {"name": "c3_attention_d64", "source": C3_ATTENTION, "interp": True,
      "function": {"name": "attention", "args": [([2, 128, 64], "f32")] * 3}},
