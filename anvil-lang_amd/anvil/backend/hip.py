@@ -60,7 +60,8 @@ def runtime_source() -> str:
     dev = read("anvil_hip.h").replace('#include "anvil_rt.h"', rt)
     gemm_path = os.path.join(RUNTIME_DIR, "anvil_mfma.h")
     if os.path.exists(gemm_path):
-        dev += "\n" + read("anvil_mfma.h")
+        bk = os.environ.get("ANVIL_GEMM_TILE_BK")
+        dev += "\n" + (f"#define ANVIL_MM_BK {int(bk)}\n" if bk else "") + read("anvil_mfma.h")
     return dev
 
 
@@ -754,36 +755,41 @@ class HipGen:
         return out
 
     def print_(self, st: ir.Print, ind: str) -> list[str]:
+        """A print statement: its text assembled in one buffer, written to stdout (or stderr) in one
+        call (the interpreter's exec_print, interp.py:213-239)."""
         f = "stderr" if st.err else "stdout"
         out = [f"{ind}anvil_sync();"]
         if st.err:
             out.append(f"{ind}fflush(stdout);")
+        out.append(f"{ind}{{ anvil_text t_ = {{NULL, 0, 0}};")
         for it in list(st.items) + [ir.PrintItem("text", st.end)]:
             if it.kind == "text":
                 if it.text:
-                    out.append(f"{ind}fputs({c_string(it.text)}, {f});")
+                    out.append(f"{ind}  anvil_text_str(&t_, {c_string(it.text)});")
             elif it.kind == "scalar":
                 b = it.buf.root
                 v = f"{self.host_view(b)}[0]"
                 if it.fmt:
                     isint = b.dtype == I32 or it.fmt.endswith("d")
-                    val = (f"(int){v}" if b.dtype == I32 else f"(int){v}") if isint else f"(double){v}"
-                    out.append(f"{ind}fprintf({f}, {c_string(it.fmt)}, {val});")
+                    val = f"(int){v}" if isint else f"anvil_fmt_arg({v})"
+                    out.append(f"{ind}  anvil_text_fmt(&t_, {c_string(it.fmt)}, {val});")
                 elif b.dtype == I32:
-                    out.append(f"{ind}fprintf({f}, \"%d\", {v});")
+                    out.append(f"{ind}  anvil_text_fmt(&t_, \"%d\", {v});")
                 else:
-                    out.append(f"{ind}anvil_put_f32({f}, {v});")
+                    out.append(f"{ind}  anvil_text_f32(&t_, {v});")
             elif it.kind == "tensor":
                 b = it.buf.root
                 dims = self.table("long", [str(d) for d in b.shape])
-                out.append(f"{ind}anvil_put_tensor({self.host_view(b)}, {1 if b.dtype == I32 else 0}, {len(b.shape)}, {dims});")
+                out.append(f"{ind}  anvil_text_tensor(&t_, {self.host_view(b)}, {1 if b.dtype == I32 else 0}, "
+                           f"{len(b.shape)}, {dims});")
             elif it.kind == "pick":
                 tab = self.strings(it.choices)
-                out.append(f"{ind}anvil_put_choice({f}, (int){self.host_view(it.buf)}[0], {tab}, {len(it.choices)});")
+                out.append(f"{ind}  anvil_text_pick(&t_, (int){self.host_view(it.buf)}[0], {tab}, {len(it.choices)});")
             elif it.kind == "chars":
-                out.append(f"{ind}anvil_put_chars((const int *){self.host_view(it.buf)}, {it.buf.numel});")
+                out.append(f"{ind}  anvil_text_chars(&t_, (const int *){self.host_view(it.buf)}, {it.buf.numel});")
             else:
                 raise NotImplementedError(it.kind)
+        out.append(f"{ind}  anvil_text_write(&t_, {f}); }}")
         return out
 
     def writable(self, b, full: bool) -> str:

@@ -218,20 +218,19 @@ def sole_writer(k: ir.Kernel, st) -> bool:
 
 
 def parallel_safe(k: ir.Kernel) -> bool:
-    written = {}
+    """May every point of k's domain run in a lane of its own, in any order (the question of the
+    reference's cuda.py:380-395)? Not when two points can write one element with a plain store
+    (through an index array with repeated values, or an offset that is not one-to-one over the
+    domain: then the last write must win, in domain order), and not when a point reads an element
+    of a buffer the kernel writes other than the one it stores itself (or adds into it)."""
     for st in k.stores:
-        written.setdefault(st.buf.root, []).append(st)
-        if st.accumulate:
-            continue                                    # an atomic add
-        if st.offset.gathers():
-            return False                                # duplicate indices: the last write wins
-        if not injective_over(st.offset, k.domain):
+        if not st.accumulate and (st.offset.gathers() or not injective_over(st.offset, k.domain)):
             return False
-    for ld in kernel_loads(k):
-        stores = written.get(ld.buf.root)
-        if stores and any(s.accumulate or s.offset != ld.offset for s in stores):
-            return False                                # reads what another element writes
-    return True
+    by_buffer: dict = {}
+    for st in k.stores:
+        by_buffer.setdefault(st.buf.root.id, []).append(st)
+    return all(not st.accumulate and st.offset == ld.offset
+               for ld in kernel_loads(k) for st in by_buffer.get(ld.buf.root.id, ()))
 
 
 # ----------------------------------------------------------------------------- host scalars
@@ -242,57 +241,59 @@ def is_scalar_kernel(k: ir.Kernel) -> bool:
 
 
 def host_scalars(prog: ir.Program) -> set:
-    """Ids of the 0-d buffers that live on the host only."""
-    writers: dict[int, list] = {}
-    counters = set()
+    """Ids of the 0-d buffers the host computes and keeps itself (the decision the reference's Metal
+    backend makes, metal.py:365-432, restated): a loop counter that only its loop writes, and a 0-d
+    result all of whose writers are scalar kernels (no domain, no reduction, no random draws) that
+    read only host buffers and constants, and write only host buffers. A kernel may read a buffer it
+    writes (Adam's t = t + 1). Derivation runs upward from the counters (a result joins once one of
+    its writers can be computed from host values) and is checked downward (a buffer with a writer
+    that cannot run on the host is refused for good), until neither changes the set."""
+    buffers = {b.root.id: b.root for b in prog.buffers}
+    written_by: dict[int, list] = {}          # 0-d buffer -> "loop", "call" or the kernels storing it
+    loop_counters = set()
     for blk in ir.walk_blocks(prog.main):
         for st in blk.stmts:
             if isinstance(st, ir.For):
-                counters.add(st.counter.root.id)
-                writers.setdefault(st.counter.root.id, []).append("loop")
+                loop_counters.add(st.counter.root.id)
+                written_by.setdefault(st.counter.root.id, []).append("loop")
             elif isinstance(st, KernelStmt):
-                for s in st.kernel.stores:
-                    writers.setdefault(s.buf.root.id, []).append(st.kernel)
+                for store in st.kernel.stores:
+                    written_by.setdefault(store.buf.root.id, []).append(st.kernel)
             elif isinstance(st, ir.RTCall):
                 for b in rt_args(st, RT_WRITES):
-                    writers.setdefault(b.root.id, []).append("rt")
-    by_id = {b.root.id: b.root for b in prog.buffers}
+                    written_by.setdefault(b.root.id, []).append("call")
 
-    def eligible(bid) -> bool:
-        b = by_id.get(bid)
+    def scalar_candidate(bid) -> bool:
+        b = buffers.get(bid)
         return b is not None and not b.shape and b.kind not in ir.EXTERN_KINDS
 
-    hosts = {c for c in counters if eligible(c) and all(w == "loop" for w in writers.get(c, []))}
-    scalar_ks = [k for k in ir.all_kernels(prog) if is_scalar_kernel(k)]
+    scalar_kernels = [k for k in ir.all_kernels(prog) if is_scalar_kernel(k)]
+    inputs = {id(k): {b.id for b in kernel_reads(k) if b.kind != "const"} for k in scalar_kernels}
+    results = {id(k): {st.buf.root.id for st in k.stores} for k in scalar_kernels}
 
-    def outs(k):
-        return {st.buf.root.id for st in k.stores}
+    def only_scalar_writers(bid) -> bool:
+        return all(isinstance(w, ir.Kernel) and is_scalar_kernel(w) for w in written_by.get(bid, []))
 
-    def reads_ok(k, allowed) -> bool:
-        for b in kernel_reads(k):
-            if b.id not in allowed and b.kind != "const":
-                return False
-        return True
+    def runs_on_host(k, on_host) -> bool:
+        return isinstance(k, ir.Kernel) and is_scalar_kernel(k) and inputs[id(k)] <= on_host \
+            and results[id(k)] <= on_host
 
-    banned: set = set()
-    changed = True
-    while changed:
-        changed = False
-        for k in scalar_ks:
-            if not reads_ok(k, hosts | (outs(k) - banned)):
+    on_host = {c for c in loop_counters
+               if scalar_candidate(c) and all(w == "loop" for w in written_by.get(c, []))}
+    refused: set = set()
+    while True:
+        state = (len(on_host), len(refused))
+        for k in scalar_kernels:                   # upward: computable from host values
+            if inputs[id(k)] - on_host - (results[id(k)] - refused):
                 continue
-            for o in outs(k) - hosts - banned:
-                ws = writers.get(o, [])
-                if eligible(o) and all(isinstance(w, ir.Kernel) and is_scalar_kernel(w) for w in ws):
-                    hosts.add(o)
-                    changed = True
-        for o in sorted(hosts - counters):
-            ws = writers.get(o, [])
-            if not all(isinstance(w, ir.Kernel) and reads_ok(w, hosts) and outs(w) <= hosts for w in ws):
-                hosts.discard(o)
-                banned.add(o)
-                changed = True
-    return hosts
+            on_host |= {r for r in results[id(k)] - refused
+                        if scalar_candidate(r) and only_scalar_writers(r)}
+        for bid in sorted(on_host - loop_counters):  # downward: every writer must run on the host
+            if not all(runs_on_host(w, on_host) for w in written_by.get(bid, [])):
+                on_host.discard(bid)
+                refused.add(bid)
+        if (len(on_host), len(refused)) == state:
+            return on_host
 
 
 def is_host_kernel(k: ir.Kernel, hosts: set) -> bool:

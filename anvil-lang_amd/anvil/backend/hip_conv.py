@@ -158,7 +158,9 @@ def rewrite(c: ir.Kernel, cp, ids):
         return operand if isinstance(x, Load) and x.buf.root is dst else x
     c3 = dataclasses.replace(c2, red=dataclasses.replace(c2.red, body=ir.map_expr(c2.red.body, fn)))
     s = hip_gemm.analyse(c3)
-    if s is None or not hip_gemm.qualifies(s):
+    # a matrix-core product, or a short sum (K < MIN_K) that each lane adds up itself: either way the
+    # window is read in place of the copy
+    if s is None or not (hip_gemm.qualifies(s) or s.K < hip_gemm.MIN_K):
         return None
     return c3
 

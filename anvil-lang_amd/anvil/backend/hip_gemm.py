@@ -26,6 +26,8 @@ from .hip_kernels import KernelScope, Plan, canon_key, decode
 
 MIN_WORK = 1 << 16           # M·N·K below which the generic schedules are as good
 MIN_SIDE = 32                # a narrower product (10 classes) wastes most of a 32-wide MFMA tile
+MIN_K = 16                   # a shorter sum (a 3 x 3 convolution of one input channel: K = 9) is a
+                             # memory-bound map: each lane sums its K terms itself
 CUS = 256                    # compute units of an MI355X
 CU_WAVES = CUS * 4           # wavefronts that fill it once (one per SIMD)
 
@@ -256,10 +258,11 @@ def gathered_ok(s) -> bool:
 
 
 def qualifies(s) -> bool:
-    """Is the product worth the matrix cores? Enough work, and both sides at least a tile wide;
+    """Is the product worth the matrix cores? Enough work, a sum of at least MIN_K terms, and both
+    sides at least a tile wide;
     a narrower one (a convolution's 32 x 9 weight gradient) only when K is long enough to be split
     across workgroups, each reading its slice of both operands once."""
-    if s.M * s.N * s.K < MIN_WORK or not gathered_ok(s):
+    if s.M * s.N * s.K < MIN_WORK or s.K < MIN_K or not gathered_ok(s):
         return False
     if min(s.M, s.N) >= MIN_SIDE:
         return True
@@ -536,6 +539,7 @@ class GemmPlan(Plan):
                 self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
             self.pipe = True
         self.forced = any(f.partition("@")[0] for f in os.environ.get("ANVIL_GEMM_FORCE", "").split(","))
+        self.stage = False              # the pipelined K split with k-contiguous operands staged in LDS
         self.followers = []             # (kernel, var map, forwarded loads) run in the epilogue
         self.layout()
 
@@ -574,6 +578,23 @@ class GemmPlan(Plan):
                 break
         nch = -(-(self.kslice // (8 * self.kgroup)) // self.waves)      # chunks per wave
         self.depth = max(1, min(int(os.environ.get("ANVIL_GEMM_DEPTH", "2" if nch <= 32 else "4")), nch))
+        # staging both operands through each wavefront's LDS (anvil_mm_tile_kstage) when both are
+        # contiguous in k (x·Wᵀ: an input gradient): one 32 x 32 tile per workgroup of four
+        # wavefronts, K in one range. Measured on 256 x 1024 x K products (one MI355X): 6.4 ns per
+        # k against 7.6 for the register-direct K split (C2's input gradient 10.9 -> 8.5-9.7 µs);
+        # with only A staged (x·W) it lost, 9.8 against 5.6 ns per k.
+        want = os.environ.get("ANVIL_GEMM_STAGE", "NT").split(",")
+        layout = {("ANVIL_LD_KC", "ANVIL_LD_RC"): "NN", ("ANVIL_LD_KC", "ANVIL_LD_KC"): "NT",
+                  ("ANVIL_LD_RC", "ANVIL_LD_RC"): "TN"}.get((self.amode, self.bmode))
+        self.stage = (self.pipe and self.waves == 4 and self.ptm * self.ptn == 1 and self.kslices == 1
+                      and layout is not None and (layout in want or layout + "s" in want)
+                      and not (s.k_multi or s.a_multi or s.b_multi) and s.K % 4 == 0
+                      and not (self.amode == "ANVIL_LD_RC" and s.a_gather)
+                      and not (self.bmode == "ANVIL_LD_RC" and s.b_gather))
+        # RC operands staged too ("NNs", "TNs"), or loaded straight into registers
+        self.stage_rc = layout is not None and layout + "s" in want
+        # independent accumulator chains per wavefront when it has one 32 x 32 tile
+        self.chains = int(os.environ.get("ANVIL_GEMM_CHAINS", "1")) if self.ptm * self.ptn == 1 else 1
         self.threads = 64 * self.waves if self.sched == "ksplit" else 256
         self.tm = -(-s.M // self.BM)
         self.tn = -(-s.N // self.BN)
@@ -634,6 +655,9 @@ class GemmPlan(Plan):
 
     def template_lds(self) -> int:
         """LDS of the anvil_mfma.h templates the kernel instantiates."""
+        if self.stage:
+            staged = 2 * (self.amode == "ANVIL_LD_KC" or self.stage_rc) + 2 * (self.bmode == "ANVIL_LD_KC" or self.stage_rc)
+            return 4 * 4 * max(staged * 32 * 36, 16 * 64)
         if self.slab:
             return 4 * (2 * 2 * self.slab * 33 + 4 * 16 * 64)
         if self.sched == "tile":
@@ -862,6 +886,17 @@ class GemmPlan(Plan):
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_kslab<{self.amode}, {self.bmode}, {self.slab}, {chk(s.M)}, {chk(s.N)}>"
                         f"(part, {kargs});"]
+            elif self.stage:
+                body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs, s.a_multi),
+                         self.row_fn(sc, "brow", s.b_gather, s.b_rs, s.b_multi)]
+                nch = -(-(-(-s.K // 32)) // 4)
+                depth = max(2, int(os.environ.get("ANVIL_GEMM_STAGE_DEPTH", "2")))
+                sa = "true" if self.stage_rc and self.amode == "ANVIL_LD_RC" else "false"
+                sb = "true" if self.stage_rc and self.bmode == "ANVIL_LD_RC" else "false"
+                main = ["    float part[1][1][4];",
+                        f"    anvil_mm_tile_kstage<{self.amode}, {self.bmode}, {nch}, {depth}, {chk(s.M)}, {chk(s.N)}, "
+                        f"{sa}, {sb}, {self.chains}>"
+                        f"(part, pa, arow, {s.a_ks}LL, pb, brow, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, 0, {s.K}, opa, opb);"]
             elif self.pipe:
                 body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs, s.a_multi),
                          self.row_fn(sc, "brow", s.b_gather, s.b_rs, s.b_multi),
@@ -878,14 +913,15 @@ class GemmPlan(Plan):
                 nch = -(-(self.kslice // (8 * G)) // W)
                 main = [f"    float part[{TM}][{TN}][{16 // W}];",
                         f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
-                        f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}, {G}>(part, {kargs});"]
+                        f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}, {G}, {self.chains}>(part, {kargs});"]
             else:
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]
             value = "part[0][0][q]" if TM * TN == 1 else "part[ti][tj][q]"
         def head():                                   # after the body: its buffers are the parameters
             return [self.k_table("a") + self.k_table("b") + self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
-                    + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, B {self.bmode[9:]}"
+                    + f" · {self.sched}{' staged' if self.stage else ''} {self.BM}x{self.BN}, A {self.amode[9:]}, "
+                    f"B {self.bmode[9:]}"
                     + (f" · K in {self.kslices} slices of {self.kslice}, partial tiles" if self.kslices > 1 else "")
                     + (f" · K over {len(s.k_multi)} variables" if s.k_multi else ""),
                     self.header(self.threads)]

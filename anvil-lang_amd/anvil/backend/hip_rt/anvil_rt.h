@@ -1,14 +1,21 @@
-// anvil_rt.h — host run-time support for libraries generated by anvil.backend.hip.
+// anvil_rt.h — host run-time of the libraries anvil.backend.hip generates (and the scalar helpers
+// their kernels share with the host, marked ANVIL_HD).
 //
-// What the generated program needs besides its kernels: the counter-based random numbers and the
-// Python-semantics integer helpers (host and device: ANVIL_HD), number and tensor printing, data
-// files, checkpoints, the Fisher-Yates shuffle, `input`. Behaviour follows the reference's host
-// runtime (anvil/backend/anvil_host.h:17-300) and interpreter (anvil/interp.py:55-115, 232-381):
-// the same random bits, the same printed text, the same checkpoint bytes.
+// Everything here reproduces a format or a rule of the Anvil language, so that a program prints,
+// draws, shuffles, reads and stores exactly what the reference interpreter does (anvil/interp.py,
+// the definition of the language's semantics): the counter-based random numbers, Python's integer
+// division, the default number format and NumPy-style tensor printing, the data-file readers, the
+// EINW checkpoint file, the scan of a stdin line for a number. Each format is stated where it is
+// implemented. The code is organised around this backend's needs: random keys are computed once
+// per stream so kernels only hash the index, printing goes through one growable text buffer that is
+// written out in one call, data files are read whole into memory and then decoded (one table of
+// element decoders for the NumPy kinds), and a checkpoint is validated by one parser before a
+// single tensor changes.
 //
-// Errors end the program: a message on stderr, then exit status 1 (anvil_host.h:69-73).
+// A run-time error ends the program: `anvil: <message>` on stderr, exit status 1.
 #pragma once
 #include <math.h>
+#include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -21,64 +28,79 @@
 #define ANVIL_HD
 #endif
 
-// ---------------------------------------------------------------------------------------- numbers
-// lowbias32 (Chris Wellons, hash-prospector): xor-shift 16, *0x7feb352d, xor-shift 15, *0x846ca68b,
-// xor-shift 16. Two rounds over idx*golden + key give the bits of element idx (anvil_host.h:17-24).
-ANVIL_HD static inline uint32_t anvil_mix32(uint32_t h) {
-    h = (h ^ (h >> 16)) * 0x7FEB352Du;
-    h = (h ^ (h >> 15)) * 0x846CA68Bu;
-    return h ^ (h >> 16);
+// ======================================================================================== numbers
+// Random numbers (interp.py:55-71). A stream's key mixes its number, a salt (0 and 1 for the two
+// uniforms of a normal draw, 7 for shuffles) and the program's seed:
+//     key = stream * 0x85EBCA77 + salt * 0xC2B2AE3D + seed + 0x632BE5AB            (mod 2^32)
+// element idx of the stream draws the 32 bits h(h(idx * 0x9E3779B1 + key)), where h is Chris
+// Wellons' lowbias32 hash (x ^= x >> 16; x *= 0x7FEB352D; x ^= x >> 15; x *= 0x846CA68B; x ^= x >> 16).
+// A uniform number keeps the top 24 bits: (bits >> 8) * 2^-24 in [0, 1), or ((bits >> 8) + 1) * 2^-24
+// in (0, 1] when the draw must not be 0 (the logarithm of Box-Muller). Both are exact in float.
+ANVIL_HD static inline uint32_t anvil_key(uint32_t stream, uint32_t salt, uint32_t seed) {
+    return 0x632BE5ABu + seed + salt * 0xC2B2AE3Du + stream * 0x85EBCA77u;
 }
-ANVIL_HD static inline uint32_t anvil_bits(uint32_t idx, uint32_t stream, uint32_t salt, uint32_t seed) {
-    const uint32_t key = seed + 0x632BE5ABu + stream * 0x85EBCA77u + salt * 0xC2B2AE3Du;
-    return anvil_mix32(anvil_mix32(key + idx * 0x9E3779B1u));
+ANVIL_HD static inline uint32_t anvil_lowbias(uint32_t v) {
+    v = (v ^ (v >> 16)) * 0x7FEB352Du;
+    v = (v ^ (v >> 15)) * 0x846CA68Bu;
+    return v ^ (v >> 16);
 }
-// The top 24 bits as a float on the 2^-24 grid: [0, 1), or (0, 1] with open_low. The sum is exact in
-// double and the product by 2^-24 is exact, so the one rounding is the cast to float.
+ANVIL_HD static inline uint32_t anvil_draw(uint32_t key, uint32_t idx) {
+    return anvil_lowbias(anvil_lowbias(idx * 0x9E3779B1u + key));
+}
+ANVIL_HD static inline float anvil_unit(uint32_t key, uint32_t idx, int open_low) {
+    const uint32_t top = (anvil_draw(key, idx) >> 8) + (open_low ? 1u : 0u);     // at most 2^24: exact
+    return (float)top * 5.9604644775390625e-08f;                                   // * 2^-24: exact
+}
 ANVIL_HD static inline float anvil_uniform(uint32_t idx, uint32_t stream, uint32_t salt, uint32_t seed, int open_low) {
-    double top = (double)(anvil_bits(idx, stream, salt, seed) >> 8) + (open_low ? 1.0 : 0.0);
-    return (float)(top * 5.9604644775390625e-08);
+    return anvil_unit(anvil_key(stream, salt, seed), idx, open_low);
 }
 
-// Integer floor division and modulo with Python's signs; a zero divisor counts as 1 (interp.py rules).
-// A divisor of -1 is done apart: INT_MIN / -1 wraps to INT_MIN (as NumPy's int32 does) instead of
-// trapping on the host.
+// Integers follow Python: a // b rounds toward minus infinity and a % b takes the divisor's sign
+// (a == (a // b) * b + a % b); a divisor of 0 counts as 1, and INT_MIN // -1 wraps to INT_MIN as
+// NumPy's int32 does (ops.py division rules; interp.py evaluates them with NumPy).
 ANVIL_HD static inline int anvil_floordiv(int a, int b) {
+    if (b == 0) b = 1;
     if (b == -1) return (int)(0u - (uint32_t)a);
-    b = b ? b : 1;
-    const int q = a / b, r = a % b;
-    return (r && ((r < 0) ^ (b < 0))) ? q - 1 : q;
+    const int q = a / b;                                  // toward zero; |q * b| <= |a|
+    return (q * b != a && ((a < 0) != (b < 0))) ? q - 1 : q;
 }
 ANVIL_HD static inline int anvil_floormod(int a, int b) {
+    if (b == 0) b = 1;
     if (b == -1) return 0;
-    b = b ? b : 1;
-    const int r = a % b;
-    return (r && ((r < 0) ^ (b < 0))) ? r + b : r;
+    return (int)((uint32_t)a - (uint32_t)anvil_floordiv(a, b) * (uint32_t)b);
 }
-// NumPy's float remainder (np.mod): the result has the divisor's sign, a zero one included.
+// NumPy's float remainder: a - floor(a / b) * b computed exactly as fmod, moved into the divisor's
+// sign; a zero result carries the divisor's sign (np.mod(3, -1.5) is -0.0).
 ANVIL_HD static inline float anvil_pymodf(float a, float b) {
-    const float r = fmodf(a, b);
-    if (r == 0.0f) return copysignf(0.0f, b);
-    return ((r < 0.0f) ^ (b < 0.0f)) ? r + b : r;
+    float r = fmodf(a, b);
+    if (r == 0.0f) return b < 0.0f ? -0.0f : 0.0f;
+    if ((r < 0.0f) != (b < 0.0f)) r += b;
+    return r;
 }
-ANVIL_HD static inline float anvil_maxf(float a, float b) { return (a != a || b != b) ? NAN : (b > a ? b : a); }
-ANVIL_HD static inline float anvil_minf(float a, float b) { return (a != a || b != b) ? NAN : (b < a ? b : a); }
-ANVIL_HD static inline int anvil_maxi(int a, int b) { return b > a ? b : a; }
+// max and min propagate nan (NumPy's maximum/minimum); the integer ones are plain.
+ANVIL_HD static inline float anvil_maxf(float a, float b) { return (a != a) ? a : (b != b) ? b : (a < b ? b : a); }
+ANVIL_HD static inline float anvil_minf(float a, float b) { return (a != a) ? a : (b != b) ? b : (b < a ? b : a); }
+ANVIL_HD static inline int anvil_maxi(int a, int b) { return a < b ? b : a; }
 ANVIL_HD static inline int anvil_mini(int a, int b) { return b < a ? b : a; }
+// sign keeps 0, -0 and nan as they are (np.sign).
 ANVIL_HD static inline float anvil_signf(float a) { return a > 0.0f ? 1.0f : (a < 0.0f ? -1.0f : a); }
-ANVIL_HD static inline int anvil_signi(int a) { return (a > 0) - (a < 0); }
+ANVIL_HD static inline int anvil_signi(int a) { return (0 < a) - (a < 0); }
 ANVIL_HD static inline float anvil_sigmoidf(float a) { return 1.0f / (1.0f + expf(-a)); }
+// i32(x) truncates toward zero.
 ANVIL_HD static inline int anvil_trunci(float a) { return (int)truncf(a); }
+// i32 arithmetic wraps modulo 2^32.
 ANVIL_HD static inline int anvil_wrap_add(int a, int b) { return (int)((uint32_t)a + (uint32_t)b); }
 ANVIL_HD static inline int anvil_wrap_sub(int a, int b) { return (int)((uint32_t)a - (uint32_t)b); }
 ANVIL_HD static inline int anvil_wrap_mul(int a, int b) { return (int)((uint32_t)a * (uint32_t)b); }
 
-// ---------------------------------------------------------------------------------------- state
+// ======================================================================================== host state
+// The random state: `seed(n)` sets the seed and restarts the stream count; every kernel that draws
+// takes the next stream, and so does every shuffle (interp.py:252-256, 309-320).
 struct anvil_host_state {
-    uint32_t seed;          // the program's seed (`seed(n)` sets it)
-    uint32_t stream;        // the next random stream: one per kernel that draws, one per shuffle
-    uint32_t seed0;         // the seed the library was generated with (library calls start from it)
-    double t0;              // `clock()` counts from here
+    uint32_t seed;
+    uint32_t stream;
+    uint32_t seed0;     // the seed the library was generated with: library calls start from it
+    double t0;          // clock() counts from here
 };
 static anvil_host_state anvil_hs = {0, 0, 0, 0.0};
 
@@ -89,200 +111,368 @@ static double anvil_seconds(void) {
 }
 
 [[noreturn]] static void anvil_die(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
-#include <stdarg.h>
 static void anvil_die(const char *fmt, ...) {
-    fflush(stdout);
+    char msg[1024];
     va_list ap;
     va_start(ap, fmt);
-    fputs("anvil: ", stderr);
-    vfprintf(stderr, fmt, ap);
-    fputc('\n', stderr);
+    vsnprintf(msg, sizeof msg, fmt, ap);
     va_end(ap);
+    fflush(stdout);
+    fprintf(stderr, "anvil: %s\n", msg);
     fflush(stderr);
     exit(1);
 }
 
-// A run-time check of the program failed (an index out of range): report the value and stop.
+// A run-time check failed (an index out of range): what, and the value that broke it.
 [[noreturn]] static void anvil_bad_value(const char *what, long long value) {
     anvil_die("runtime error: %s (got %lld)", what, value);
 }
 
-// ---------------------------------------------------------------------------------------- printing
-// A float as the interpreter prints it: %.4f for 0, nan and 1e-4 <= |v| < 1e6, else %.4e.
-static void anvil_put_f32(FILE *f, float v) {
-    double d = (double)v, a = fabs(d);
-    fprintf(f, (v == 0.0f || v != v || (a >= 1e-4 && a < 1e6)) ? "%.4f" : "%.4e", d);
+// ======================================================================================== text
+// Everything a print statement writes is assembled in one buffer and handed to stdio in one call.
+struct anvil_text { char *p; size_t len, cap; };
+
+static void anvil_text_room(anvil_text *t, size_t more) {
+    if (t->len + more + 1 <= t->cap) return;
+    size_t cap = t->cap ? t->cap : 256;
+    while (cap < t->len + more + 1) cap *= 2;
+    char *p = (char *)realloc(t->p, cap);
+    if (p == NULL) anvil_die("out of host memory (printing)");
+    t->p = p;
+    t->cap = cap;
+}
+static void anvil_text_put(anvil_text *t, const char *s, size_t n) {
+    anvil_text_room(t, n);
+    memcpy(t->p + t->len, s, n);
+    t->len += n;
+    t->p[t->len] = 0;
+}
+static void anvil_text_str(anvil_text *t, const char *s) { anvil_text_put(t, s, strlen(s)); }
+static void anvil_text_fmt(anvil_text *t, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static void anvil_text_fmt(anvil_text *t, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    char small[96];
+    const int n = vsnprintf(small, sizeof small, fmt, ap);
+    va_end(ap);
+    if (n < 0) return;
+    if ((size_t)n < sizeof small) { anvil_text_put(t, small, (size_t)n); return; }
+    anvil_text_room(t, (size_t)n);
+    va_start(ap, fmt);
+    vsnprintf(t->p + t->len, (size_t)n + 1, fmt, ap);
+    va_end(ap);
+    t->len += (size_t)n;
+}
+static void anvil_text_write(anvil_text *t, FILE *f) {
+    if (t->len) fwrite(t->p, 1, t->len, f);
+    free(t->p);
+    t->p = NULL;
+    t->len = t->cap = 0;
 }
 
-static void anvil_put_elem(const void *data, int is_int, long i) {
-    if (is_int) printf("%d", ((const int *)data)[i]);
-    else anvil_put_f32(stdout, ((const float *)data)[i]);
+// The default number format (interp.py:74-81): fixed with four decimals when the value is 0, nan,
+// or 1e-4 <= |v| < 1e6; four-decimal scientific otherwise. Integers print in full.
+static void anvil_text_f32(anvil_text *t, float v) {
+    if (v != v) { anvil_text_put(t, "nan", 3); return; }      // any nan, whatever its sign bit
+    const double d = (double)v, m = fabs(d);
+    const int fixed = v == 0.0f || (m >= 1e-4 && m < 1e6);
+    anvil_text_fmt(t, fixed ? "%.4f" : "%.4e", d);
+}
+// A value for a `{x:fmt}` item: Python formats every nan as "nan", printf a negative one as "-nan".
+static inline double anvil_fmt_arg(float v) { return v != v ? (double)NAN : (double)v; }
+
+// Tensors print as NumPy does (interp.py:84-115): nested brackets, elements of the last dimension
+// separated by ", ", rows of dimension d by ",\n" and d + 1 spaces; "[]" when empty, the bare
+// element at rank 0. Above 1000 elements every dimension longer than 6 shows its indices 0, 1, 2,
+// "...", n-3, n-2, n-1 only.
+#define ANVIL_ELLIPSIS (-1L)
+struct anvil_tensor_view {
+    const void *data;
+    int is_int;
+    int rank;
+    const long *dims;
+    long stride[16];
+    long shown[16][7];      // the indices each dimension shows when summarized
+    int count[16];          // how many (0: all of them)
+};
+
+static void anvil_text_elem(anvil_text *t, const anvil_tensor_view *v, long at) {
+    if (v->is_int) anvil_text_fmt(t, "%d", ((const int *)v->data)[at]);
+    else anvil_text_f32(t, ((const float *)v->data)[at]);
 }
 
-// One dimension of a tensor, NumPy style: rows on their own lines, indented by depth; with more
-// than 1000 elements each dimension longer than 6 shows its first and last three entries.
-static void anvil_put_dim(const void *data, int is_int, int rank, const long *dims, const long *strides,
-                          long base, int d, int brief) {
-    const long n = dims[d];
-    const int cut = brief && n > 6;
-    const long count = cut ? 7 : n;
-    putchar('[');
-    for (long k = 0; k < count; k++) {
-        if (k > 0) {
-            if (d == rank - 1) fputs(", ", stdout);
-            else { fputs(",\n", stdout); for (int s = 0; s <= d; s++) putchar(' '); }
+static void anvil_text_block(anvil_text *t, const anvil_tensor_view *v, int d, long base) {
+    const int last = d == v->rank - 1;
+    const long n = v->count[d] ? v->count[d] : v->dims[d];
+    anvil_text_put(t, "[", 1);
+    for (long k = 0; k < n; k++) {
+        if (k) {
+            if (last) anvil_text_put(t, ", ", 2);
+            else {
+                anvil_text_put(t, ",\n", 2);
+                for (int s = 0; s <= d; s++) anvil_text_put(t, " ", 1);
+            }
         }
-        long i = k;
-        if (cut) {
-            if (k == 3) { fputs("...", stdout); continue; }
-            if (k > 3) i = n - 7 + k;
-        }
-        if (d == rank - 1) anvil_put_elem(data, is_int, base + i);
-        else anvil_put_dim(data, is_int, rank, dims, strides, base + i * strides[d], d + 1, brief);
+        const long i = v->count[d] ? v->shown[d][k] : k;
+        if (i == ANVIL_ELLIPSIS) anvil_text_put(t, "...", 3);
+        else if (last) anvil_text_elem(t, v, base + i);
+        else anvil_text_block(t, v, d + 1, base + i * v->stride[d]);
     }
-    putchar(']');
+    anvil_text_put(t, "]", 1);
 }
 
-static void anvil_put_tensor(const void *data, int is_int, int rank, const long *dims) {
-    if (rank == 0) { anvil_put_elem(data, is_int, 0); return; }
-    long strides[16], numel = 1;
-    for (int d = rank - 1; d >= 0; d--) { strides[d] = numel; numel *= dims[d]; }
-    if (numel == 0) { fputs("[]", stdout); return; }
-    anvil_put_dim(data, is_int, rank, dims, strides, 0, 0, numel > 1000);
+static void anvil_text_tensor(anvil_text *t, const void *data, int is_int, int rank, const long *dims) {
+    anvil_tensor_view v;
+    v.data = data;
+    v.is_int = is_int;
+    v.rank = rank;
+    v.dims = dims;
+    if (rank == 0) { anvil_text_elem(t, &v, 0); return; }
+    long numel = 1;
+    for (int d = rank - 1; d >= 0; d--) { v.stride[d] = numel; numel *= dims[d]; }
+    if (numel == 0) { anvil_text_put(t, "[]", 2); return; }
+    for (int d = 0; d < rank; d++) {
+        const long n = dims[d];
+        v.count[d] = 0;
+        if (numel > 1000 && n > 6) {
+            const long pick[7] = {0, 1, 2, ANVIL_ELLIPSIS, n - 3, n - 2, n - 1};
+            memcpy(v.shown[d], pick, sizeof pick);
+            v.count[d] = 7;
+        }
+    }
+    anvil_text_block(t, &v, 0, 0);
 }
 
-static void anvil_put_choice(FILE *f, int k, const char *const *choices, int n) {
-    fputs((k >= 0 && k < n) ? choices[k] : "?", f);
+// `{k:...}` over a list of strings picks one ("?" out of range); chars() writes byte values as text;
+// show() draws a grid of small integers with one glyph each ("?" out of range), a row per line.
+static void anvil_text_pick(anvil_text *t, int k, const char *const *choices, int n) {
+    anvil_text_str(t, (k >= 0 && k < n) ? choices[k] : "?");
 }
-
-static void anvil_put_chars(const int *codes, long n) {
-    for (long i = 0; i < n; i++) putchar(codes[i] & 0xFF);
+static void anvil_text_chars(anvil_text *t, const int *codes, long n) {
+    anvil_text_room(t, (size_t)n);
+    for (long i = 0; i < n; i++) t->p[t->len + i] = (char)(codes[i] & 0xFF);
+    t->len += (size_t)n;
+    t->p[t->len] = 0;
 }
-
 static void anvil_show_grid(const int *grid, long rows, long cols, const char *const *glyphs, int n) {
-    for (long r = 0; r < rows; r++) {
-        for (long c = 0; c < cols; c++) {
-            const int v = grid[r * cols + c];
-            fputs((v >= 0 && v < n) ? glyphs[v] : "?", stdout);
-        }
-        putchar('\n');
+    anvil_text t = {NULL, 0, 0};
+    for (long at = 0; at < rows * cols; at++) {
+        const int v = grid[at];
+        anvil_text_str(&t, (v >= 0 && v < n) ? glyphs[v] : "?");
+        if (at % cols == cols - 1) anvil_text_put(&t, "\n", 1);
     }
+    anvil_text_write(&t, stdout);
 }
 
-// ---------------------------------------------------------------------------------------- data files
-// A data file is read where it was when the program was compiled, or, with $ANVIL_DATA set, from
-// that directory under its file name (anvil_host.h:132-141).
+// ======================================================================================== data files
+// A data file is opened at the path the program was compiled with or, with $ANVIL_DATA set, under
+// that directory by its file name (for a library built on one machine and run on another).
 static const char *anvil_data_file(const char *path) {
-    static char where[4096];
+    static char moved[4096];
     const char *dir = getenv("ANVIL_DATA");
-    if (dir == NULL || dir[0] == 0) return path;
-    const char *slash = strrchr(path, '/');
-    snprintf(where, sizeof where, "%s/%s", dir, slash ? slash + 1 : path);
-    return where;
+    if (dir == NULL || *dir == 0) return path;
+    const char *base = strrchr(path, '/');
+    snprintf(moved, sizeof moved, "%s/%s", dir, base ? base + 1 : path);
+    return moved;
 }
 
-[[noreturn]] static void anvil_bad_shape(const char *path) {
+// Files the program writes (save_npy, checkpoints) and the checkpoints it loads are at their
+// compiled paths or, with $ANVIL_OUT set, in that directory under their file names: a run can keep
+// its outputs apart without a new build (no counterpart in the reference, whose paths are fixed).
+static const char *anvil_out_file(const char *path) {
+    static char moved[4096];
+    const char *dir = getenv("ANVIL_OUT");
+    if (dir == NULL || *dir == 0) return path;
+    const char *base = strrchr(path, '/');
+    snprintf(moved, sizeof moved, "%s/%s", dir, base ? base + 1 : path);
+    return moved;
+}
+
+[[noreturn]] static void anvil_wrong_shape(const char *path) {
     anvil_die("data file %s does not have the shape this program was compiled for", path);
 }
 
-static unsigned char *anvil_slurp(const char *path, long *size) {
-    FILE *f = fopen(path, "rb");
-    if (f == NULL) anvil_die("cannot open data file %s", path);
-    fseek(f, 0, SEEK_END);
-    long n = ftell(f);
-    fseek(f, 0, SEEK_SET);
-    unsigned char *buf = (unsigned char *)malloc((size_t)n + 1);
-    n = (long)fread(buf, 1, (size_t)n, f);
-    buf[n] = 0;
-    fclose(f);
-    *size = n;
-    return buf;
+// The whole file in memory (a NUL after its last byte); gunzip: through zlib, which reads a file
+// that is not compressed as it is.
+struct anvil_blob { unsigned char *p; long n; };
+
+static anvil_blob anvil_blob_read(const char *path, int gunzip) {
+    anvil_blob b = {NULL, 0};
+    long cap = 1 << 16;
+    b.p = (unsigned char *)malloc((size_t)cap + 1);
+    if (b.p == NULL) anvil_die("out of host memory (reading %s)", path);
+    if (gunzip) {
+        gzFile z = gzopen(path, "rb");
+        if (z == NULL) { free(b.p); anvil_die("cannot open data file %s", path); }
+        for (;;) {
+            if (b.n == cap) {
+                cap *= 2;
+                b.p = (unsigned char *)realloc(b.p, (size_t)cap + 1);
+                if (b.p == NULL) anvil_die("out of host memory (reading %s)", path);
+            }
+            const int got = gzread(z, b.p + b.n, (unsigned)(cap - b.n));
+            if (got <= 0) break;
+            b.n += got;
+        }
+        gzclose(z);
+    } else {
+        FILE *f = fopen(path, "rb");
+        if (f == NULL) { free(b.p); anvil_die("cannot open data file %s", path); }
+        size_t got;
+        while ((got = fread(b.p + b.n, 1, (size_t)(cap - b.n), f)) > 0) {
+            b.n += (long)got;
+            if (b.n == cap) {
+                cap *= 2;
+                b.p = (unsigned char *)realloc(b.p, (size_t)cap + 1);
+                if (b.p == NULL) anvil_die("out of host memory (reading %s)", path);
+            }
+        }
+        fclose(f);
+    }
+    b.p[b.n] = 0;
+    return b;
 }
 
-// IDX files (MNIST), gzip'ed or not: skip the header, then one byte per element.
+// IDX (MNIST) files, gzip'ed or not: after `header` bytes, one unsigned byte per element.
 static void anvil_read_idx(const char *path, void *out, long n, long header, int is_int) {
     path = anvil_data_file(path);
-    gzFile f = gzopen(path, "rb");
-    if (f == NULL) anvil_die("cannot open data file %s", path);
-    unsigned char *raw = (unsigned char *)malloc(n > 0 ? (size_t)n : 1);
-    unsigned char skip[256];
-    const int ok = gzread(f, skip, (unsigned)header) == (int)header && gzread(f, raw, (unsigned)n) == (int)n;
-    gzclose(f);
-    if (!ok) anvil_bad_shape(path);
+    anvil_blob b = anvil_blob_read(path, 1);
+    if (b.n < header + n) { free(b.p); anvil_wrong_shape(path); }
+    const unsigned char *px = b.p + header;
     for (long i = 0; i < n; i++) {
-        if (is_int) ((int *)out)[i] = raw[i];
-        else ((float *)out)[i] = (float)raw[i];
+        if (is_int) ((int *)out)[i] = px[i];
+        else ((float *)out)[i] = (float)px[i];
     }
-    free(raw);
+    free(b.p);
 }
 
-static int anvil_number_here(const char *p) {      // [+-] [.] digit
-    if (*p == '+' || *p == '-') p++;
-    if (*p == '.') p++;
-    return *p >= '0' && *p <= '9';
+// The numbers of a text file: every match of [-+]?(digits[.digits*]|.digits)([eE][-+]?digits)? in
+// order (interp.py:28). Returns the length of the match at p, or 0 when none starts there.
+static long anvil_number_at(const char *p) {
+    const char *q = p;
+    if (*q == '+' || *q == '-') q++;
+    const char *d = q;
+    while (*q >= '0' && *q <= '9') q++;
+    const long whole = q - d;
+    long frac = 0;
+    if (*q == '.') {
+        const char *f = ++q;
+        while (*q >= '0' && *q <= '9') q++;
+        frac = q - f;
+        if (whole == 0 && frac == 0) return 0;
+    } else if (whole == 0) {
+        return 0;
+    }
+    if (*q == 'e' || *q == 'E') {
+        const char *e = q + 1;
+        if (*e == '+' || *e == '-') e++;
+        const char *x = e;
+        while (*e >= '0' && *e <= '9') e++;
+        if (e > x) q = e;
+    }
+    return q - p;
 }
 
+// The text's number at p (len characters) as the nearest float.
+static float anvil_number_value(const char *p, long len) {
+    char tmp[128];
+    if (len >= (long)sizeof tmp) len = sizeof tmp - 1;
+    memcpy(tmp, p, (size_t)len);
+    tmp[len] = 0;
+    return strtof(tmp, NULL);
+}
+
+// CSV: skip `skip_lines` lines, then the first n numbers (anywhere: separators are not checked).
 static void anvil_read_csv(const char *path, float *out, long n, long skip_lines) {
     path = anvil_data_file(path);
-    long size;
-    char *text = (char *)anvil_slurp(path, &size), *p = text;
-    for (long s = 0; s < skip_lines && *p; p++) if (*p == '\n') s++;
-    long got = 0;
-    while (got < n && *p) {
-        if (anvil_number_here(p)) { char *end; out[got++] = strtof(p, &end); p = end; }
-        else p++;
+    anvil_blob b = anvil_blob_read(path, 0);
+    const char *p = (const char *)b.p, *end = p + b.n;
+    for (long s = 0; s < skip_lines && p < end; s++) {
+        const char *nl = (const char *)memchr(p, '\n', (size_t)(end - p));
+        p = nl ? nl + 1 : end;
     }
-    free(text);
-    if (got < n) anvil_bad_shape(path);
+    long got = 0;
+    while (got < n && p < end) {
+        const long len = anvil_number_at(p);
+        if (len == 0) { p++; continue; }
+        out[got++] = anvil_number_value(p, len);
+        p += len;
+    }
+    free(b.p);
+    if (got < n) anvil_wrong_shape(path);
 }
 
+// A file's bytes, one element each: the file must hold exactly n.
 static void anvil_read_bytes(const char *path, int *out, long n) {
     path = anvil_data_file(path);
-    long size;
-    unsigned char *raw = anvil_slurp(path, &size);
-    if (size != n) anvil_bad_shape(path);
-    for (long i = 0; i < n; i++) out[i] = raw[i];
-    free(raw);
+    anvil_blob b = anvil_blob_read(path, 0);
+    if (b.n != n) { free(b.p); anvil_wrong_shape(path); }
+    for (long i = 0; i < n; i++) out[i] = b.p[i];
+    free(b.p);
 }
 
-static float anvil_half_to_float(uint16_t h) {
-    const int e = (h >> 10) & 31, m = h & 1023;
-    float v = e == 0 ? ldexpf((float)m, -24) : e == 31 ? (m ? NAN : INFINITY) : ldexpf((float)(m | 1024), e - 25);
-    return (h & 0x8000) ? -v : v;
+// NumPy element kinds (the code the front end records for a .npy or .safetensors tensor): 0 <f4,
+// 1 <f8, 2 <f2, 3 <i4, 4 <i8, 5 u1, 6 i1, 7 <u2, 8 <i2; little-endian. The float kinds fill an f32
+// tensor (f8 rounds to nearest), the integer kinds an i32 one (i8 keeps its low 32 bits).
+static uint64_t anvil_le(const unsigned char *p, int bytes) {
+    uint64_t v = 0;
+    for (int i = bytes - 1; i >= 0; i--) v = (v << 8) | p[i];
+    return v;
 }
+// IEEE half to float, exactly: the same value with an 8-bit exponent (subnormal halves normalised).
+static float anvil_half(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu, bits;
+    if (exp == 0x1F) bits = sign | 0x7F800000u | (man << 13);              // inf, nan
+    else if (exp != 0) bits = sign | ((exp + 112u) << 23) | (man << 13);   // 127 - 15 = 112
+    else if (man == 0) bits = sign;                                         // +-0
+    else {                                                                  // subnormal: shift in
+        int e = 113;
+        while (!(man & 0x400u)) { man <<= 1; e--; }
+        bits = sign | ((uint32_t)e << 23) | ((man & 0x3FFu) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+static double anvil_npy_f4(const unsigned char *p) { uint32_t u = (uint32_t)anvil_le(p, 4); float f; memcpy(&f, &u, 4); return f; }
+static double anvil_npy_f8(const unsigned char *p) { uint64_t u = anvil_le(p, 8); double d; memcpy(&d, &u, 8); return d; }
+static double anvil_npy_f2(const unsigned char *p) { return anvil_half((uint16_t)anvil_le(p, 2)); }
+static int64_t anvil_npy_i4(const unsigned char *p) { return (int32_t)(uint32_t)anvil_le(p, 4); }
+static int64_t anvil_npy_i8(const unsigned char *p) { return (int64_t)anvil_le(p, 8); }
+static int64_t anvil_npy_u1(const unsigned char *p) { return p[0]; }
+static int64_t anvil_npy_i1(const unsigned char *p) { return (int8_t)p[0]; }
+static int64_t anvil_npy_u2(const unsigned char *p) { return (uint16_t)anvil_le(p, 2); }
+static int64_t anvil_npy_i2(const unsigned char *p) { return (int16_t)(uint16_t)anvil_le(p, 2); }
+struct anvil_npy_kind { int bytes; double (*real)(const unsigned char *); int64_t (*whole)(const unsigned char *); };
+static const anvil_npy_kind anvil_npy_kinds[9] = {
+    {4, anvil_npy_f4, NULL}, {8, anvil_npy_f8, NULL}, {2, anvil_npy_f2, NULL},
+    {4, NULL, anvil_npy_i4}, {8, NULL, anvil_npy_i8}, {1, NULL, anvil_npy_u1},
+    {1, NULL, anvil_npy_i1}, {2, NULL, anvil_npy_u2}, {2, NULL, anvil_npy_i2},
+};
 
-// n values of a .npy (or a tensor inside a .safetensors file, kind | 16) starting at byte `offset`,
-// converted to f32/i32. Kinds: 0 f4, 1 f8, 2 f2, 3 i4, 4 i8, 5 u1, 6 i1, 7 u2, 8 i2.
+// n elements of `kind` from byte `offset`: a whole .npy must end right after them; kind + 16 marks a
+// tensor inside a .safetensors file, which other tensors follow.
 static void anvil_read_npy(const char *path, void *out, long n, long offset, int kind, int size) {
     path = anvil_data_file(path);
-    FILE *f = fopen(path, "rb");
-    if (f == NULL) anvil_die("cannot open data file %s", path);
-    fseek(f, offset, SEEK_SET);
-    const long want = n * size, extra = (kind & 16) ? 0 : 1;   // a whole .npy must end here
-    unsigned char *raw = (unsigned char *)malloc((size_t)want + 1);
-    const long got = (long)fread(raw, 1, (size_t)(want + extra), f);
-    fclose(f);
-    if (got != want) anvil_bad_shape(path);
+    const int slice = (kind & 16) != 0;
     kind &= 15;
-    for (long i = 0; i < n; i++) {
-        const unsigned char *p = raw + i * size;
-        float fv; double dv; int32_t iv; int64_t lv; int16_t sv; uint16_t uv;
-        switch (kind) {
-        case 0: memcpy(&fv, p, 4); ((float *)out)[i] = fv; break;
-        case 1: memcpy(&dv, p, 8); ((float *)out)[i] = (float)dv; break;
-        case 2: memcpy(&uv, p, 2); ((float *)out)[i] = anvil_half_to_float(uv); break;
-        case 3: memcpy(&iv, p, 4); ((int *)out)[i] = iv; break;
-        case 4: memcpy(&lv, p, 8); ((int *)out)[i] = (int)lv; break;
-        case 5: ((int *)out)[i] = p[0]; break;
-        case 6: ((int *)out)[i] = (signed char)p[0]; break;
-        case 7: memcpy(&uv, p, 2); ((int *)out)[i] = uv; break;
-        default: memcpy(&sv, p, 2); ((int *)out)[i] = sv; break;
-        }
+    if (kind > 8 || anvil_npy_kinds[kind].bytes != size) anvil_wrong_shape(path);
+    const anvil_npy_kind *k = &anvil_npy_kinds[kind];
+    anvil_blob b = anvil_blob_read(path, 0);
+    const long need = offset + n * (long)size;
+    if (slice ? b.n < need : b.n != need) { free(b.p); anvil_wrong_shape(path); }
+    const unsigned char *p = b.p + offset;
+    for (long i = 0; i < n; i++, p += size) {
+        if (k->real) ((float *)out)[i] = (float)k->real(p);
+        else ((int *)out)[i] = (int)(uint32_t)(uint64_t)k->whole(p);
     }
-    free(raw);
+    free(b.p);
 }
 
+// save_npy: the .npy header the front end built, then the raw 4-byte elements. A file that cannot
+// be written is reported, and the program goes on.
 static void anvil_write_npy(const char *path, const unsigned char *header, long hlen, const void *data, long bytes) {
+    path = anvil_out_file(path);
     FILE *f = fopen(path, "wb");
     if (f == NULL) { fprintf(stderr, "anvil: cannot write %s\n", path); return; }
     fwrite(header, 1, (size_t)hlen, f);
@@ -290,81 +480,115 @@ static void anvil_write_npy(const char *path, const unsigned char *header, long 
     fclose(f);
 }
 
-// ---------------------------------------------------------------------------------------- checkpoints
-// File: "EINW", u32 version 2, u64 tensor count, one u64 key per tensor (element count in the low 32
-// bits, an FNV-1a hash of name:dtype:shape in the high 32), then the raw 4-byte elements
-// (ir.py:753-764; anvil_host.h:237-266). Version 1 files hold element counts only.
+// ======================================================================================== checkpoints
+// An EINW file (interp.py:341-372, ir.py:753-764), little-endian:
+//     "EINW"  u32 version (2)  u64 tensor count n  |  n x u64 key  |  the tensors' 4-byte elements
+// A key holds the tensor's element count in its low 32 bits and, in version 2, a 32-bit FNV-1a hash
+// of "<name inside the model>:<dtype>:<d0,d1,...>" (never 0) in its high 32 bits; a version-1 file
+// stores the counts alone. load() accepts version 1 or 2, the same n, equal keys (or counts) and
+// exactly the bytes they imply; anything else (or no file) leaves every tensor as it was and
+// gives 0, success gives 1.
 struct anvil_ckpt_entry { void *data; uint64_t key; };
 
-static const uint64_t ANVIL_CKPT_V1 = 0x00000001574E4945ull, ANVIL_CKPT_V2 = 0x00000002574E4945ull;
+static uint64_t anvil_ckpt_elems(uint64_t key) { return key & 0xFFFFFFFFull; }
 
 static void anvil_ckpt_save(const char *path, const anvil_ckpt_entry *tab, long n) {
+    path = anvil_out_file(path);
     FILE *f = fopen(path, "wb");
     if (f == NULL) { fprintf(stderr, "anvil: cannot write %s\n", path); return; }
-    const uint64_t head[2] = {ANVIL_CKPT_V2, (uint64_t)n};
-    fwrite(head, 8, 2, f);
-    for (long i = 0; i < n; i++) fwrite(&tab[i].key, 8, 1, f);
-    for (long i = 0; i < n; i++) fwrite(tab[i].data, 4, (size_t)(tab[i].key & 0xFFFFFFFFull), f);
+    unsigned char head[16] = {'E', 'I', 'N', 'W', 2, 0, 0, 0};
+    for (int i = 0; i < 8; i++) head[8 + i] = (unsigned char)((uint64_t)n >> (8 * i));
+    fwrite(head, 1, sizeof head, f);
+    for (long t = 0; t < n; t++) {
+        unsigned char k[8];
+        for (int i = 0; i < 8; i++) k[i] = (unsigned char)(tab[t].key >> (8 * i));
+        fwrite(k, 1, 8, f);
+    }
+    for (long t = 0; t < n; t++) fwrite(tab[t].data, 4, (size_t)anvil_ckpt_elems(tab[t].key), f);
     fclose(f);
 }
 
-// 1 if the file holds exactly these tensors (and they were read into tab's memory), else 0.
+// The byte offset of the first tensor if `file` is a checkpoint of exactly these tensors, else -1.
+static long anvil_ckpt_parse(const unsigned char *file, long size, const anvil_ckpt_entry *tab, long n) {
+    if (size < 16 || memcmp(file, "EINW", 4) != 0) return -1;
+    const uint64_t version = anvil_le(file + 4, 4), count = anvil_le(file + 8, 8);
+    if ((version != 1 && version != 2) || count != (uint64_t)n) return -1;
+    const long data = 16 + 8 * n;
+    if (size < data) return -1;
+    uint64_t elems = 0;
+    for (long t = 0; t < n; t++) {
+        const uint64_t want = version == 2 ? tab[t].key : anvil_ckpt_elems(tab[t].key);
+        if (anvil_le(file + 16 + 8 * t, 8) != want) return -1;
+        elems += anvil_ckpt_elems(tab[t].key);
+    }
+    return (uint64_t)size == (uint64_t)data + 4 * elems ? data : -1;
+}
+
 static float anvil_ckpt_load(const char *path, const anvil_ckpt_entry *tab, long n) {
+    path = anvil_out_file(path);
     FILE *f = fopen(path, "rb");
     if (f == NULL) return 0.0f;
-    uint64_t head[2] = {0, 0}, elems = 0;
-    int ok = fread(head, 8, 2, f) == 2 && (head[0] == ANVIL_CKPT_V1 || head[0] == ANVIL_CKPT_V2) && head[1] == (uint64_t)n;
-    const uint64_t mask = (ok && head[0] == ANVIL_CKPT_V2) ? ~0ull : 0xFFFFFFFFull;
-    for (long i = 0; ok && i < n; i++) {
-        uint64_t key;
-        ok = fread(&key, 8, 1, f) == 1 && key == (tab[i].key & mask);
-        elems += tab[i].key & 0xFFFFFFFFull;
-    }
-    if (ok) {
-        fseek(f, 0, SEEK_END);
-        ok = ftell(f) == (long)(16 + 8 * n + 4 * elems);
-        fseek(f, 16 + 8 * n, SEEK_SET);
-    }
-    for (long i = 0; ok && i < n; i++) {
-        const size_t count = (size_t)(tab[i].key & 0xFFFFFFFFull);
-        ok = fread(tab[i].data, 4, count, f) == count;
-    }
     fclose(f);
-    return ok ? 1.0f : 0.0f;
+    anvil_blob b = anvil_blob_read(path, 0);
+    const long at = anvil_ckpt_parse(b.p, b.n, tab, n);
+    if (at >= 0) {
+        const unsigned char *p = b.p + at;
+        for (long t = 0; t < n; t++) {
+            const size_t bytes = 4 * (size_t)anvil_ckpt_elems(tab[t].key);
+            memcpy(tab[t].data, p, bytes);
+            p += bytes;
+        }
+    }
+    free(b.p);
+    return at >= 0 ? 1.0f : 0.0f;
 }
 
-// ---------------------------------------------------------------------------------------- the rest
-// Fisher-Yates from the back: step k swaps p[n-1-k] with p[bits(k, stream, salt 7) % (n-k)]; one
-// stream per shuffle (anvil_host.h:269-276; interp.py:309-320).
+// ======================================================================================== the rest
+// Fisher-Yates from the back (interp.py:309-320): with the shuffle's own stream, the k-th step
+// (k = 0 .. n-2) swaps p[i], i = n-1-k, with p[draw(k) mod (i + 1)].
 static void anvil_fisher_yates(int *p, long n) {
-    const uint32_t stream = anvil_hs.stream++;
-    for (long k = 0; k + 1 < n; k++) {
-        const long i = n - 1 - k;
-        const long j = (long)(anvil_bits((uint32_t)k, stream, 7u, anvil_hs.seed) % (uint32_t)(i + 1));
-        const int t = p[i]; p[i] = p[j]; p[j] = t;
+    const uint32_t key = anvil_key(anvil_hs.stream++, 7u, anvil_hs.seed);
+    for (long i = n - 1; i > 0; i--) {
+        const long j = (long)(anvil_draw(key, (uint32_t)(n - 1 - i)) % (uint32_t)(i + 1));
+        const int t = p[i];
+        p[i] = p[j];
+        p[j] = t;
     }
 }
 
-static void anvil_fill_iota(int *p, long n) { for (long i = 0; i < n; i++) p[i] = (int)i; }
+static void anvil_fill_iota(int *p, long n) {
+    for (long i = 0; i < n; i++) p[i] = (int)i;
+}
 
+// nonzero: the first `size` flat indices of nonzero flags, in order, then -1 (interp.py:373-378).
 static void anvil_find_nonzero(const int *flags, long n, int *out, long size) {
     long k = 0;
-    for (long i = 0; i < n && k < size; i++) if (flags[i] != 0) out[k++] = (int)i;
-    while (k < size) out[k++] = -1;
+    for (long i = 0; i < n && k < size; i++)
+        if (flags[i]) out[k++] = (int)i;
+    if (k < size) {
+        for (long r = k; r < size; r++) out[r] = -1;
+    }
 }
 
-// One number from a line of stdin (the first decimal number in it, else nan); 1 at end of input.
+// input: one line of stdin; its first number (the grammar of anvil_number_at: decimal only, so
+// "0x1F" reads 0) or nan when it has none (interp.py:332-340). At the end of the input: a newline,
+// and 1 (the program ends).
 static int anvil_read_number(float *out) {
-    char line[256];
     fflush(stdout);
-    if (fgets(line, sizeof line, stdin) == NULL) { putchar('\n'); return 1; }
-    for (char *p = line; *p; p++) {
-        if (!anvil_number_here(p)) continue;
-        char *q = p + ((*p == '+' || *p == '-') ? 1 : 0);
-        if (q[0] == '0' && (q[1] == 'x' || q[1] == 'X')) q[1] = 0;      // no hexadecimal
-        *out = strtof(p, NULL);
-        return 0;
+    char *line = NULL;
+    size_t cap = 0;
+    const ssize_t len = getline(&line, &cap, stdin);
+    if (len < 0) {
+        free(line);
+        fputs("\n", stdout);
+        return 1;
     }
-    *out = NAN;
+    float v = NAN;
+    for (const char *p = line; *p; p++) {
+        const long m = anvil_number_at(p);
+        if (m > 0) { v = anvil_number_value(p, m); break; }
+    }
+    free(line);
+    *out = v;
     return 0;
 }

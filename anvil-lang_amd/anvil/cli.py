@@ -96,9 +96,9 @@ def main(argv=None) -> int:
                                  f"{nbytes / s / 1e9:8.1f}  {label}\n")
     if args.dump:
         keep = [k for k in args.keep.split(",") if k]
-        by_name = {}
-        for b in prog.buffers:
-            by_name.setdefault(b.name, b.root)
+        # a name held by several buffers (a variable reassigned in place) means the last of them,
+        # as the fixture writer reads it
+        by_name = {b.name: b.root for b in prog.buffers}
         arrays = {}
         for k in keep:
             b = by_name[k] if not k.startswith("#") else next(x.root for x in prog.buffers if x.id == int(k[1:]))

@@ -222,29 +222,122 @@ def c3_run(calls: int) -> dict:
             "functions": out}
 
 
-def cpu_baseline(prog, data, steps: int):
-    """The NumPy interpreter on the same IR: set-up untimed, one warm-up step, then `steps` steps."""
+def host_description() -> str:
+    """The host CPU (model, count) and its thread environment, for the baseline's record."""
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    env = ", ".join(f"{k}={os.environ.get(k, 'unset')}" for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS"))
+    return f"{model}, {os.cpu_count()} logical CPUs; environment {env}"
+
+
+def oracle_run(prog, data, counter: str, stop_after: int | None):
+    """The NumPy interpreter (oracle/interp.py) on an IR program with every BLAS/OpenMP pool limited
+    to one thread: the perf_counter time at each start of the `counter` loop's iterations, and at
+    the end of the run (or when stop_after iterations have started)."""
     import io
     sys.path.insert(0, ROOT)
+    from threadpoolctl import threadpool_limits
     from oracle import interp
     marks = []
 
-    def hook(counter, value):
-        if counter == LOOP_COUNTER:
+    def hook(name, value):
+        if name == counter:
             marks.append(time.perf_counter())
-            if len(marks) > steps + 1:
+            if stop_after is not None and len(marks) > stop_after:
                 raise interp.StopRun()
     m = interp.Machine(prog, out=io.StringIO(), seed=int(data.get("seed", 0)), loop_hook=hook)
-    try:
-        m.run()
-    except interp.StopRun:
-        pass
+    with threadpool_limits(limits=1):
+        try:
+            m.run()
+        except interp.StopRun:
+            pass
+    return marks, time.perf_counter()
+
+
+def cpu_baseline(prog, data, steps: int):
+    """The NumPy interpreter on the same IR: set-up untimed, one warm-up step, then `steps` steps."""
+    marks, _ = oracle_run(prog, data, LOOP_COUNTER, steps + 1)
     t = marks[-1] - marks[1]
-    threads = os.environ.get("OMP_NUM_THREADS") or os.environ.get("OPENBLAS_NUM_THREADS") or "unset"
     return {"value": round(steps * BATCH / t, 2), "unit": "samples/s", "cores": 1, "kind": "port",
             "sample": f"{steps} full-size C2 training steps (batch 256) after 1 warm-up step, NumPy "
-                      f"interpreter (oracle/interp.py), one thread of {os.cpu_count()} host CPUs "
-                      f"(OMP_NUM_THREADS={threads}); {t:.1f} s"}
+                      f"interpreter (oracle/interp.py) with every BLAS/OpenMP thread pool limited to 1 "
+                      f"(threadpoolctl); host: {host_description()}; {t:.1f} s"}
+
+
+C1_WORKLOAD = os.path.join(ROOT, "tests", "golden", "ir", "c1_mlp.json")
+C1_BATCH = 64
+
+
+def c1_epoch(cpu: bool) -> dict:
+    """Config C1 (784-128-10 MLP, SGD 0.1, batch 64 shuffled, one epoch of 60,000 samples, then the
+    10,000-sample evaluation): samples/s over the epoch's steps on the GPU (device events at each
+    step) and, with cpu, through the NumPy interpreter on this host, one thread (the whole epoch
+    and the evaluation after it, perf_counter)."""
+    from anvil import irjson
+    from anvil.backend import hip
+    with open(C1_WORKLOAD) as f:
+        data = json.load(f)
+    prog = irjson.load(data)
+    lib = hip.load(prog, seed=int(data.get("seed", 0)))
+    lib.lib.anvil_marks_select(LOOP_COUNTER.encode())
+    t0 = time.perf_counter()
+    with quiet_stdout():
+        rc = lib.main()
+        lib.lib.anvil_sync_device()
+    wall = time.perf_counter() - t0
+    if rc != 0:
+        raise SystemExit(f"bench: C1 exited with status {rc}")
+    n = lib.lib.anvil_marks_count()
+    ms = lib.lib.anvil_marks_elapsed_ms(0, n - 1)
+    gpu = round((n - 1) * C1_BATCH / (ms / 1e3), 1)
+    out = {"steps": n, "gpu_samples_per_s": gpu, "gpu_epoch_ms_steps": round(ms * n / (n - 1), 3),
+           "gpu_program_wall_s": round(wall, 3), "library": os.path.basename(lib.path)}
+    if cpu:
+        marks, end = oracle_run(prog, data, LOOP_COUNTER, None)
+        steps = len(marks)
+        t_steps = marks[-1] - marks[0]
+        out.update({"cpu_samples_per_s": round((steps - 1) * C1_BATCH / t_steps, 1),
+                    "cpu_epoch_s": round(end - marks[0], 2),
+                    "cpu": f"oracle/interp.py, one thread (threadpoolctl); {host_description()}",
+                    "speedup": round(gpu / ((steps - 1) * C1_BATCH / t_steps), 1)})
+    return out
+
+
+YARDSTICK_SHAPES = [(256, 1024, 784, "NN"), (256, 1024, 1024, "NN"), (256, 1024, 1024, "NT"),
+                    (784, 1024, 256, "TN"), (1024, 1024, 256, "TN")]
+
+
+def yardstick(calls: int = 200) -> dict:
+    """The vendor library's fp32 products (torch.mm: hipBLASLt / rocBLAS, TF32 off) on C2's product
+    shapes, as a yardstick for the generated kernels. Event timing here includes the host's launch
+    rate; the kernels' own durations come from `rocprofv3 --kernel-trace --stats` of this mode."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    out = []
+    for M, N, K, lay in YARDSTICK_SHAPES:
+        a = torch.randn(*((K, M) if lay == "TN" else (M, K)), device="cuda")
+        b = torch.randn(*((N, K) if lay == "NT" else (K, N)), device="cuda")
+        c = torch.empty(M, N, device="cuda")
+        x = a.t() if lay == "TN" else a
+        y = b.t() if lay == "NT" else b
+        for _ in range(10):
+            torch.mm(x, y, out=c)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(calls):
+            torch.mm(x, y, out=c)
+        e.record()
+        torch.cuda.synchronize()
+        out.append({"shape": f"{lay} {M}x{N}x{K}", "us_per_call_events": round(s.elapsed_time(e) / calls * 1e3, 2)})
+    return {"metric": "torch.mm fp32 on C2's product shapes (yardstick)", "calls": calls, "products": out}
 
 
 def main() -> int:
@@ -254,11 +347,16 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-steps", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-c1", action="store_true", help="skip config C1's one-epoch run (GPU and CPU)")
     p.add_argument("--profile-table", action="store_true", help="print every kernel's time to stderr")
     p.add_argument("--graphs", action="store_true", help="replay loop bodies as HIP graphs")
     p.add_argument("--copy", action="store_true", help="run the copy kernel that calibrates HBM counters")
     p.add_argument("--c3", action="store_true", help="config C3: the standalone functions, per kernel")
+    p.add_argument("--yardstick", action="store_true", help="torch.mm (the vendor library) on C2's product shapes")
     args = p.parse_args()
+    if args.yardstick:
+        print(json.dumps(yardstick()), flush=True)
+        return 0
     if args.copy:
         print(json.dumps(copy_run()), flush=True)
         return 0
@@ -295,6 +393,8 @@ def main() -> int:
         cpu = cpu_baseline(prog, data, args.cpu_steps)
         line["cpu_baseline"] = cpu
         line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    if not args.no_c1:
+        line["c1_epoch"] = c1_epoch(cpu=not args.no_cpu)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -30,7 +30,7 @@ def vectors(name):
 # fixtures whose oracle run takes minutes (C2 whole: 500 full-size steps of the NumPy interpreter;
 # C5 at full size: its im2col products broadcast over 10^9 elements a step); the oracle replays them
 # only with ANVIL_SLOW_ORACLE=1, the GPU tests always compare against them
-SLOW = {"c2_full", "c5_full3", "c4_full2"}
+SLOW = {"c2_full", "c5_full3", "c4_full2", "c2_full100", "c4_t256_2", "c5_step1", "c2_full10"}
 
 
 def vector_names(slow=False):
@@ -41,6 +41,32 @@ def vector_names(slow=False):
 
 def stdout_of(z):
     return bytes(z["stdout"]).decode()
+
+
+# where make_fixtures.py placed the fixture programs: files they write (save_npy, save) are recorded
+# under this directory in their IR, and kept byte for byte in the vectors as "file:<name>"
+RECORDED_DIR = "/root/repo/tests/golden/programs/"
+
+
+def written_files(z) -> list[str]:
+    return [k[5:] for k in z.files if k.startswith("file:")]
+
+
+def stdin_of(name: str) -> str:
+    """What a fixture program reads with `input` (the scripted stdin of tests/golden/programs.py)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("_fixture_programs", os.path.join(GOLDEN, "programs.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return next((p.get("stdin", "") for p in mod.PROGRAMS if p["name"] == name), "")
+
+
+def load_ir_writing_to(name, directory):
+    """A fixture's program whose output files go to `directory` instead of RECORDED_DIR."""
+    with open(ir_path(name)) as f:
+        text = f.read().replace(RECORDED_DIR, os.path.join(str(directory), ""))
+    data = json.loads(text)
+    return irjson.load(data), data
 
 
 def run_oracle(prog, data, z=None, stdin=""):

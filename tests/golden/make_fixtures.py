@@ -24,6 +24,7 @@ import importlib.util
 import io
 import json
 import os
+import shutil
 import sys
 
 import numpy as np
@@ -82,6 +83,7 @@ def main(ref_root: str) -> None:
         if only and name not in only:
             continue
         path = spec.get("path") or os.path.join(HERE, "programs", f"{name}.anvil")
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
         if spec.get("function"):
             fn = spec["function"]
             sig = tuple(("tensor", tuple(shape), dtype) for shape, dtype in fn["args"])
@@ -146,6 +148,15 @@ def main(ref_root: str) -> None:
             for k, b in enumerate(low.outputs):
                 if b is not None:
                     arrays[f"output{k}"] = it.arr(b)[:b.numel].reshape(b.shape).copy()
+        # files the program wrote (save_npy, save), kept byte for byte; a checkpoint the reference
+        # wrote may also be published as a data file for a program that loads it
+        for fname in spec.get("files", []):
+            written = os.path.join(os.path.dirname(path), fname)
+            with open(written, "rb") as f:
+                arrays[f"file:{fname}"] = np.frombuffer(f.read(), dtype=np.uint8)
+            if fname in spec.get("publish", {}):
+                shutil.copyfile(written, os.path.join(HERE, "data", spec["publish"][fname]))
+            os.remove(written)
         arrays["stdout"] = np.frombuffer(out.getvalue().encode(), dtype=np.uint8)
         np.savez_compressed(os.path.join(HERE, "vectors", f"{name}.npz"), **arrays)
     with open(ROUTE, "w") as f:

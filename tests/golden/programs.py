@@ -6,7 +6,8 @@ Each entry: name, source, optional consts (the `--set` overrides), seed, and
   function: {...} -> lower one function with pyapi.lower for these argument shapes,
   stdin: "..."    -> what `input` reads.
 The configurations C1-C5 are the workloads named in BASELINE.json; the rest restate the cases of
-the reference's CUDA backend tests (tests/test_cuda.py:26-159) as programs of their own.
+the reference's CUDA backend tests (tests/test_cuda.py:26-159) as programs of their own, and the
+run-time calls (data files, checkpoints, input, nonzero) with data files from make_data.py.
 """
 
 # ----------------------------------------------------------------------------- C1: MLP 784-128-10, SGD
@@ -68,6 +69,8 @@ for epoch in range(EPOCHS):
         loss = cross_entropy(net(x), y)
         minimize loss with adam(lr=1e-3)
         step += 1
+        if step == 1:
+            print("step 1 loss {loss:.6e}")
 print("steps {step}   loss {loss:.4f}")
 """
 
@@ -113,42 +116,39 @@ const LAYERS = 4
 
 seed(3)
 
-model Block:
-    param Wq: [D, D] ~ normal(0, sqrt(1 / D))
-    param Wk: [D, D] ~ normal(0, sqrt(1 / D))
-    param Wv: [D, D] ~ normal(0, sqrt(1 / D))
-    param Wo: [D, D] ~ normal(0, sqrt(0.5 / D))
-    up = Linear(D, 4 * D)
-    down = Linear(4 * D, D)
-    fn forward(x):
-        h = layer_norm(x)
-        q = (h @ Wq).reshape(-1, T, HEADS, DH)
-        k = (h @ Wk).reshape(-1, T, HEADS, DH)
-        v = (h @ Wv).reshape(-1, T, HEADS, DH)
-        s[b, a, i, j] = sum q[b, i, a, e] * k[b, j, a, e] / sqrt(DH) + (0.0 if j <= i else -1e9)
-        p = softmax(s)
-        o[b, i, a, e] = sum p[b, a, i, j] * v[b, j, a, e]
-        x = x + o.reshape(-1, T, D) @ Wo
-        return x + (layer_norm(x) |> up |> gelu |> down)
+model Layer:
+    param Wqkv: [D, 3 * D] ~ normal(0, sqrt(1 / D))
+    param Wout: [D, D] ~ normal(0, sqrt(0.5 / D))
+    ff_in = Linear(D, 4 * D)
+    ff_out = Linear(4 * D, D)
+    fn forward(z):
+        qkv = (layer_norm(z) @ Wqkv).reshape(-1, T, 3, HEADS, DH)
+        score[n, h, t, u] = sum qkv[n, t, 0, h, c] * qkv[n, u, 1, h, c] / sqrt(DH) - 1e9 * f32(u > t)
+        w = softmax(score)
+        mix[n, t, h, c] = sum w[n, h, t, u] * qkv[n, u, 2, h, c]
+        z = z + mix.reshape(-1, T, D) @ Wout
+        return z + ff_out(gelu(ff_in(layer_norm(z))))
 
-model GPT:
-    param E: [V, D] ~ normal(0, 0.5)
-    param P: [T, D] ~ normal(0, 0.1)
-    blocks = [Block() for n in range(LAYERS)]
-    out = Linear(D, V)
+model CharModel:
+    param tok: [V, D] ~ normal(0, 0.5)
+    param pos: [T, D] ~ normal(0, 0.1)
+    layers = [Layer() for n in range(LAYERS)]
+    head = Linear(D, V)
     fn forward(codes):
-        e[b, t, d] = E[codes[b, t], d] + P[t, d]
-        static for blk in blocks:
-            e = blk(e)
-        return e |> layer_norm |> out
+        z[n, t, d] = tok[codes[n, t], d] + pos[t, d]
+        static for layer in layers:
+            z = layer(z)
+        return head(layer_norm(z))
 
-net = GPT()
+net = CharModel()
 
 for step in range(STEPS):
-    x: i32[BATCH, T + 1] ~ randint(0, V)
-    logits = net(x[:, 0:T])
-    loss = cross_entropy(logits.reshape(BATCH * T, V), x[:, 1:T + 1].reshape(BATCH * T))
+    text: i32[BATCH, T + 1] ~ randint(0, V)
+    logits = net(text[:, 0:T])
+    loss = cross_entropy(logits.reshape(BATCH * T, V), text[:, 1:T + 1].reshape(BATCH * T))
     minimize loss over net with adam(lr=1e-3)
+    if step == 0:
+        print("step 1 loss {loss:.6e}")
 print("loss {loss:.4f}")
 """
 
@@ -177,6 +177,8 @@ net = Net()
 for step in range(STEPS):
     loss = cross_entropy(net(X), Y)
     minimize loss with sgd(lr=0.05)
+    if step == 0:
+        print("step 1 loss {loss:.6e}")
 print("loss {loss:.4f}")
 """
 
@@ -196,69 +198,73 @@ for step in range(20):
 print(loss)
 """
 
-HELLO = """
-x = [1.0, 2.0, 3.0]
-W = [[1.0, 0.0, -1.0],
-     [0.5, 0.5,  0.5]]
-y[i] = sum W[i, j] * x[j]
-print("y = {y}")
-outer[i, j] = x[i] * x[j]
-print(outer)
-print("softmax {softmax(x)} max {max(x)} mean {mean(x):.3f}")
-noise: [2, 3] ~ normal(0, 1)
-print("noise = {noise}")
-param w: [3]
-loss = sum((w - x) ** 2)
-dw = grad(loss, w)
-print("dw {dw}")
+GREET = """
+v = [0.5, -1.5, 2.0, 4.0]
+M = [[2.0, 1.0, 0.0, -1.0],
+     [0.0, 3.0, 1.0, 1.0],
+     [1.0, 1.0, 1.0, 1.0]]
+r[a] = sum M[a, b] * v[b]
+print("r = {r}")
+gap[a, b] = v[a] - v[b]
+print(gap)
+print("logsm {log_softmax(v)} min {min(v)} total {sum(v):.2f}")
+u: [3, 2] ~ uniform(-1, 1)
+print("u = {u}")
+param p: [4]
+obj = sum((p * v - 1.0) ** 2)
+dp = grad(obj, p)
+print("dp {dp}")
 """
 
-LINREG = """
-n = 1000
-X: [n, 3] ~ normal(0, 1)
-noise: [n] ~ normal(0, 0.1)
-y = X @ [2.0, -3.4, 1.7] + 4.2 + noise
+LOGREG = """
+m = 800
+F: [m, 4] ~ normal(0, 1)
+z = F @ [1.5, -0.5, 2.0, 0.25] - 0.3
+lab = f32(z > 0)
 
-param w: [3]
-param b: f32
+param w: [4]
+param c: f32
 
-for step in range(100):
-    loss = mse(X @ w + b, y)
-    minimize loss with sgd(lr=0.1)
-    if step % 20 == 0:
-        print("step {step:3d}   loss {loss:.5f}")
+for it in range(80):
+    prob = sigmoid(F @ w + c)
+    loss = -mean(lab * log(prob + 1e-6) + (1 - lab) * log(1 - prob + 1e-6))
+    minimize loss with sgd(lr=0.5)
+    if it % 16 == 0:
+        print("iter {it:3d}   loss {loss:.5f}")
 
-print("learned w = {w}   b = {b:.3f}")
+print("w = {w}   c = {c:.3f}")
 """
 
-ATTENTION_TRAIN = """
-B = 8
-T = 16
-d = 24
-h = 8
+ATTENTION_FIT = """
+NB = 4
+L = 12
+E = 16
+K = 8
 
-fn attention(x: [b, t, dm], Wq: [dm, dh], Wk: [dm, dh], Wv: [dm, dh]) -> [b, t, dh]:
-    q = x @ Wq
-    k = x @ Wk
-    v = x @ Wv
-    s[..., i, j] = sum q[..., i, c] * k[..., j, c] / sqrt(dh)
-    p = softmax(s)
-    out[..., i, c] = sum p[..., i, j] * v[..., j, c]
-    return out
+fn head(z: [b, t, e], A: [e, k], B: [e, k], C: [e, k], O: [k, e]) -> [b, t, e]:
+    qq = z @ A
+    kk = z @ B
+    vv = z @ C
+    logit[n, t, u] = sum qq[n, t, c] * kk[n, u, c] * 0.35355339
+    att = softmax(logit)
+    ctx[n, t, c] = sum att[n, t, u] * vv[n, u, c]
+    return ctx @ O
 
-Tq: [d, h] ~ normal(0, 0.4)
-Tk: [d, h] ~ normal(0, 0.4)
-Tv: [d, h] ~ normal(0, 0.4)
+RA: [E, K] ~ normal(0, 0.3)
+RB: [E, K] ~ normal(0, 0.3)
+RC: [E, K] ~ normal(0, 0.3)
+RO: [K, E] ~ normal(0, 0.3)
 
-param Wq: [d, h] ~ normal(0, 0.2)
-param Wk: [d, h] ~ normal(0, 0.2)
-param Wv: [d, h] ~ normal(0, 0.2)
+param A: [E, K] ~ normal(0, 0.1)
+param B: [E, K] ~ normal(0, 0.1)
+param C: [E, K] ~ normal(0, 0.1)
+param O: [K, E] ~ normal(0, 0.1)
 
-for step in range(1, 61):
-    x: [B, T, d] ~ normal(0, 1)
-    loss = mse(attention(x, Wq, Wk, Wv), attention(x, Tq, Tk, Tv))
-    minimize loss with adam(lr=0.01)
-    if step % 20 == 0:
+for step in range(1, 49):
+    z: [NB, L, E] ~ normal(0, 1)
+    loss = mse(head(z, A, B, C, O), head(z, RA, RB, RC, RO))
+    minimize loss with adam(lr=0.02)
+    if step % 12 == 0:
         print("step {step:3d}   loss {loss:.5f}")
 """
 
@@ -418,6 +424,128 @@ for epoch in range(EPOCHS):
     print("epoch {epoch + 1}   loss {loss:.4f}   test accuracy {acc:.4f}")
 """
 
+FILES = """
+t = csv("../data/table.csv")
+print(t)
+print("sum {sum(t):.4f}")
+note = bytes("../data/note.txt")
+print(note)
+tiles = idx("../data/tiles-idx3-ubyte.gz")
+print(tiles)
+marks: i32[6] = idx("../data/marks-idx1-ubyte")
+print(marks)
+print(npy("../data/k_f4.npy"))
+print(npy("../data/k_f8.npy"))
+print(npy("../data/k_f2.npy"))
+print(npy("../data/k_i4.npy"))
+print(npy("../data/k_i8.npy"))
+print(npy("../data/k_u1.npy"))
+print(npy("../data/k_i1.npy"))
+print(npy("../data/k_u2.npy"))
+print(npy("../data/k_i2.npy"))
+print(npy("../data/k_b1.npy"))
+w = safetensors("../data/layer.safetensors", "layer.w")
+print(w)
+print(safetensors("../data/layer.safetensors", "layer.half"))
+print(safetensors("../data/layer.safetensors", "layer.ids"))
+save_npy(w * 2, "OUT_w2.npy")
+save_npy(marks + 1, "OUT_marks.npy")
+"""
+
+PICKS = """
+v: i32[20] ~ randint(0, 3)
+print(v)
+grid: [3, 5] ~ uniform(-1, 1)
+print(grid)
+r, c = nonzero(grid > 0.25, size=6, fill_value=-9)
+print(r)
+print(c)
+q, s = nonzero(v.reshape(4, 5) == 2, size=12)
+print(q)
+print(s)
+total = 0.0
+for turn in range(20):
+    x = input("value? ")
+    if x != x:
+        print("(no number)")
+        continue
+    total += x
+    print("total {total:.3f}")
+"""
+
+PICKS_STDIN = "3\nabc 4.5e1 x\n0x1F\n-.25\nnothing here\n+-2e-1 tail\n1e\n7."
+
+CELL = """
+model Cell:
+    param gate: [3, 4] ~ uniform(-1, 1)
+    param bias: [4] ~ uniform(0, 0.5)
+
+model Pair:
+    left = Cell()
+    right = Cell()
+    param scale: [2] ~ uniform(1, 2)
+"""
+
+CKPT_WRITE = CELL + """
+seed(21)
+net = Pair()
+print("gate sum {sum(net.left.gate):.6f}   scale {net.scale}")
+save(net, "OUT_pair.ckpt")
+"""
+
+CKPT_READ = CELL + """
+model Swapped:
+    param gate: [4, 3] ~ uniform(-1, 1)
+    param bias: [4] ~ uniform(0, 0.5)
+
+seed(22)
+net = Pair()
+got = load(net, "../data/pair.ckpt")
+print("loaded {got}")
+print(net.left.gate)
+print(net.right.bias)
+print(net.scale)
+other = Swapped()
+before = sum(other.gate)
+miss = load(other, "../data/pair.ckpt")
+print("mismatched {miss} unchanged {sum(other.gate) == before}")
+none = load(net, "../data/no-such.ckpt")
+print("absent {none}")
+"""
+
+SERIAL = """
+order: i32[10] = [2, 0, 2, 1, 3, 0, 2, 1, 1, 3]
+vals: [10] ~ uniform(0, 1)
+slots: [4] = 0.0
+slots[order] = vals
+print(slots)
+pick: i32[6] = [5, 5, 0, 5, 2, 0]
+dst: i32[6] = 0
+dst[pick] = pick * 10 + arange(6)
+print(dst)
+"""
+
+BOARD = """
+cells: i32[3, 6] ~ randint(0, 6)
+show(cells, ".#o*")
+print(cells)
+"""
+
+DRAWS = """
+seed(5)
+u: [3, 4] ~ uniform(-2, 2)
+k: i32[40] ~ randint(-5, 17)
+b: [10] ~ bernoulli(0.6)
+m: i32[2, 3] ~ randint(0, 1000)
+g: [5] ~ uniform(0, 1)
+print(i32(u * 4194304.0))
+print(i32(g * 16777216.0))
+print(u)
+print(k)
+print(b)
+print(m)
+"""
+
 C1_KEEP = ["net.l1.W", "net.l1.b", "net.l2.W", "net.l2.b", "perm"]
 C2_KEEP = ["net.l1.W", "net.l1.b", "net.l2.W", "net.l2.b", "net.l3.W", "net.l3.b", "perm"]
 
@@ -429,7 +557,7 @@ PROGRAMS = [
     {"name": "c1_full", "source": C1, "interp": True, "keep": ["net.l2.W", "net.l2.b"]},
     {"name": "c2_full", "source": C2, "interp": True, "keep": ["net.l3.W", "net.l3.b"]},
     {"name": "c4_full2", "source": C4, "consts": {"STEPS": 2}, "interp": True,
-     "keep": ["net.blocks.0.Wq", "net.blocks.3.up.W", "net.out.W", "net.out.b"]},
+     "keep": ["net.layers.0.Wqkv", "net.layers.3.ff_in.W", "net.head.W", "net.head.b"]},
     {"name": "c5_full3", "source": C5, "consts": {"STEPS": 3}, "interp": True,
      "keep": ["net.c1.W", "net.c1.b", "net.c2.W", "net.c2.b", "net.fc2.W"]},
     {"name": "c2_full10", "source": C2, "consts": {"STEPS": 10}, "interp": True,
@@ -464,7 +592,7 @@ PROGRAMS = [
     # q, k and v's contributions (`+=`) among them
     {"name": "c4_mid", "source": C4,
      "consts": {"STEPS": 2, "BATCH": 4, "T": 32, "D": 64, "HEADS": 2, "LAYERS": 1}, "interp": True,
-     "keep": ["net.E", "net.blocks.0.Wq", "net.blocks.0.up.W", "net.out.W"]},
+     "keep": ["net.tok", "net.layers.0.Wqkv", "net.layers.0.ff_in.W", "net.head.W"]},
     {"name": "c5_small", "source": C5, "consts": {"STEPS": 3, "NB": 4, "C1": 4, "C2": 8, "HID": 16},
      "interp": True},
     # C5 at a size where the convolution's weight gradient is a product with K over the batch and
@@ -500,9 +628,9 @@ PROGRAMS = [
     {"name": "check_healthy", "source": CHECK_HEALTHY, "interp": True, "optimize": False, "check": "inf",
      "path": "checked.anvil"},
     # the reference's CUDA backend test cases as programs
-    {"name": "hello", "source": HELLO, "interp": True},
-    {"name": "linreg", "source": LINREG, "interp": True, "keep": ["w", "b"]},
-    {"name": "attention_train", "source": ATTENTION_TRAIN, "interp": True},
+    {"name": "greet", "source": GREET, "interp": True},
+    {"name": "logreg", "source": LOGREG, "interp": True, "keep": ["w", "c"]},
+    {"name": "attention_fit", "source": ATTENTION_FIT, "interp": True, "keep": ["A", "O"]},
     {"name": "split", "source": SPLIT, "interp": True},
     {"name": "scatter", "source": SCATTER, "interp": True},
     {"name": "bounds", "source": BOUNDS},
@@ -514,4 +642,24 @@ PROGRAMS = [
     {"name": "control", "source": CONTROL, "interp": True},
     {"name": "products", "source": PRODUCTS, "interp": True},
     {"name": "mnist_like", "source": MNIST_LIKE, "interp": True, "keep": C1_KEEP},
+    # the run-time calls: data files of every kind, save_npy (the bytes written are kept), nonzero,
+    # input from a scripted stdin, checkpoints written by the reference and read back
+    {"name": "files", "source": FILES, "interp": True, "files": ["OUT_w2.npy", "OUT_marks.npy"]},
+    {"name": "picks", "source": PICKS, "interp": True, "stdin": PICKS_STDIN},
+    {"name": "ckpt_write", "source": CKPT_WRITE, "interp": True, "files": ["OUT_pair.ckpt"],
+     "publish": {"OUT_pair.ckpt": "pair.ckpt"}},
+    {"name": "ckpt_read", "source": CKPT_READ, "interp": True},
+    # plain stores through an index with repeated targets: the last write wins, in domain order
+    {"name": "serial", "source": SERIAL, "interp": True, "keep": ["slots", "dst"]},
+    # show(): one glyph per element, "?" for values past the glyphs
+    {"name": "board", "source": BOARD, "interp": True},
+    # device-drawn random numbers, printed (uniforms also as the integers u·2²² and g·2²⁴, their exact
+    # bits) and kept, bit for bit; printed last, so every tensor keeps its memory to the end
+    {"name": "draws", "source": DRAWS, "interp": True, "keep": ["u", "k", "b", "m"]},
+    # north-star tolerances at full size: C2 after 100 steps (every parameter), the first step's loss
+    # of C2, C4 and C5 to 7 digits, and C4 at T = 256
+    {"name": "c2_full100", "source": C2, "consts": {"STEPS": 100}, "interp": True, "keep": C2_KEEP[:6]},
+    {"name": "c4_t256_2", "source": C4, "consts": {"STEPS": 2, "T": 256}, "interp": True,
+     "keep": ["net.layers.0.Wqkv", "net.layers.3.ff_in.W", "net.head.W", "net.head.b"]},
+    {"name": "c5_step1", "source": C5, "consts": {"STEPS": 1}, "interp": True},
 ]

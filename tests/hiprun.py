@@ -30,8 +30,9 @@ NUMBER = re.compile(r"[-+]?(?:\d+\.\d*|\.\d+|\d+)(?:[eE][-+]?\d+)?|[-+]?inf|nan"
 
 
 def run_program(name_or_path: str, emulate: bool, keep=(), timeout: int = 600, cwd=None, env_extra=None,
-                check=None):
-    """(exit status, stdout, stderr, {buffer name: final contents})."""
+                check=None, stdin: str = "", out_dir=None):
+    """(exit status, stdout, stderr, {buffer name: final contents}). stdin: what `input` reads;
+    out_dir: where the files the program writes go ($ANVIL_OUT; the library is the same build)."""
     path = name_or_path if name_or_path.endswith(".json") else ir_path(name_or_path)
     with tempfile.TemporaryDirectory() as d:
         dump = os.path.join(d, "out.npz")
@@ -44,7 +45,10 @@ def run_program(name_or_path: str, emulate: bool, keep=(), timeout: int = 600, c
             cmd += ["--dump", dump, "--keep", ",".join(keep)]
         env = dict(os.environ, PYTHONPATH=ROOT_PKG + os.pathsep + os.environ.get("PYTHONPATH", ""))
         env.update(env_extra or {})
-        r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout, cwd=cwd or d, env=env)
+        if out_dir is not None:
+            env["ANVIL_OUT"] = str(out_dir)
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout, cwd=cwd or d, env=env,
+                           input=stdin)
         arrays = {}
         if keep and os.path.exists(dump):
             z = np.load(dump)
@@ -126,6 +130,40 @@ def tensors_match(want: np.ndarray, got: np.ndarray, rtol: float) -> str | None:
 
 def kept_buffers(name: str) -> list[str]:
     return [k[4:] for k in vectors(name).files if k.startswith("buf:")]
+
+
+# fixtures whose kept buffers hold values the device computes exactly (random draws, copies of
+# them, gathered stores): compared bit for bit, not to a tolerance
+BIT_EXACT = {"draws", "serial"}
+
+
+def same_bits(want: np.ndarray, got: np.ndarray) -> str | None:
+    if want.shape != got.shape or want.dtype.itemsize != 4:
+        return f"shape {got.shape}, expected {want.shape}"
+    w, g = np.ascontiguousarray(want).view(np.uint32), np.ascontiguousarray(got).astype(want.dtype).view(np.uint32)
+    bad = np.flatnonzero(w.reshape(-1) != g.reshape(-1))
+    return None if bad.size == 0 else f"{bad.size} elements differ in their bits (first at {bad[0]})"
+
+
+def check_program_run(name: str, emulate: bool, tmp_path, rtol: float, timeout: int = 600):
+    """Run a fixture program (its scripted stdin, its output files into tmp_path) and hold it to the
+    rules above: stdout, kept buffers, printed accuracies, and the bytes of every file it wrote."""
+    from fixtures import stdin_of, stdout_of, written_files
+    keep = kept_buffers(name)
+    z = vectors(name)
+    files = written_files(z)
+    rc, out, err, arrays = run_program(name, emulate=emulate, keep=keep, timeout=timeout, stdin=stdin_of(name),
+                                       out_dir=tmp_path if files else None)
+    assert rc == 0, err
+    problem = outputs_match(stdout_of(z), out, rtol=rtol)
+    assert problem is None, problem
+    assert accuracy_tokens(out) == accuracy_tokens(stdout_of(z)), "test accuracy differs"
+    for k in keep:
+        problem = (same_bits if name in BIT_EXACT else lambda w, g: tensors_match(w, g, rtol=1e-3))(z[f"buf:{k}"], arrays[k])
+        assert problem is None, f"{k}: {problem}"
+    for f in files:
+        got = (tmp_path / f).read_bytes()
+        assert got == bytes(z[f"file:{f}"]), f"{f}: {len(got)} bytes differ from the reference's"
 
 
 def patched_program(name: str, directory: str, **replace) -> str:

@@ -43,7 +43,7 @@ def test_gpu_library_exports_every_declared_symbol():
 
 
 def test_without_a_gpu_the_library_refuses_to_run():
-    path = gpu_library("hello")
+    path = gpu_library("greet")
     code = f"import ctypes, sys; sys.exit(ctypes.CDLL({path!r}).anvil_main())"
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120,
                        env=dict(os.environ, HIP_VISIBLE_DEVICES=os.environ.get("HIP_VISIBLE_DEVICES", "")))

@@ -6,30 +6,24 @@ products with fused epilogues), the device arena, host scalars and the fault lat
 were written by the reference interpreter (tests/golden/make_fixtures.py); the libraries are built
 by __graft_entry__.build() (they are looked up by the hash of their source).
 """
+import re
+
 import numpy as np
 import pytest
 
 import closed_forms
 from fixtures import load_ir, stdout_of, vectors
-from hiprun import accuracy_tokens, function_call, kept_buffers, outputs_match, patched_program, run_program, tensors_match
+from hiprun import (accuracy_tokens, check_program_run, function_call, kept_buffers, outputs_match, run_program,
+                    tensors_match)
 from test_hip_emulate import FUNCTIONS, PROGRAMS, TRAINED
 
 pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("name", PROGRAMS)
-def test_gpu_program_matches_reference(name):
+def test_gpu_program_matches_reference(name, tmp_path):
     print(f"gpu program {name}", flush=True)
-    keep = kept_buffers(name)
-    rc, out, err, arrays = run_program(name, emulate=False, keep=keep, timeout=300)
-    assert rc == 0, err
-    z = vectors(name)
-    problem = outputs_match(stdout_of(z), out, rtol=1e-3 if name in TRAINED else 1e-4)
-    assert problem is None, problem
-    assert accuracy_tokens(out) == accuracy_tokens(stdout_of(z)), "test accuracy differs"
-    for k in keep:
-        problem = tensors_match(z[f"buf:{k}"], arrays[k], rtol=1e-3)
-        assert problem is None, f"{k}: {problem}"
+    check_program_run(name, emulate=False, tmp_path=tmp_path, rtol=1e-3 if name in TRAINED else 1e-4, timeout=300)
 
 
 @pytest.mark.parametrize("name", ["c1_full", "c2_full", "c2_full10", "c4_full2", "c5_full3"])
@@ -63,6 +57,9 @@ def test_gpu_full_size_program_matches_reference(name):
     z = vectors(name)
     problem = outputs_match(stdout_of(z), out, rtol=2e-3 if name == "c2_full" else 1e-3)
     assert problem is None, problem
+    if _step1_loss(stdout_of(z)) is not None:
+        want, got = _step1_loss(stdout_of(z)), _step1_loss(out)
+        assert abs(got - want) <= 1e-4 * abs(want), f"step-1 loss {got} vs {want}"
     assert accuracy_tokens(out) == accuracy_tokens(stdout_of(z)), "test accuracy differs"
     for k in keep:
         ref, got = z[f"buf:{k}"].astype(np.float64), arrays[k].astype(np.float64)
@@ -78,6 +75,47 @@ def test_gpu_full_size_program_matches_reference(name):
         else:
             problem = tensors_match(z[f"buf:{k}"], arrays[k], rtol=1e-3)
             assert problem is None, f"{k}: {problem}"
+
+
+def _step1_loss(text):
+    m = re.search(r"step 1 loss (\S+)", text)
+    return None if m is None else float(m.group(1))
+
+
+@pytest.mark.parametrize("name", ["c2_full100", "c4_t256_2", "c5_step1"])
+def test_gpu_north_star_tolerances(name):
+    """BASELINE.json's north-star bars at full size, against the reference interpreter's runs:
+      - the first training step's loss of C2, C4 (at T = 256) and C5, printed to 7 digits, within
+        rel 1e-4 (c2_full100, c4_t256_2, c5_step1; every C2/C4 fixture prints it too);
+      - C2's weights W1, W2, W3 after 100 full-size Adam steps within rel 1e-3 of each tensor's
+        largest value; its biases, which start at 0 and move by about lr per step whatever the
+        gradient's size, against lr·steps (as for c2_full10), 99 % of them to 1 % and all to 5 %;
+      - C4 at T = 256 for 2 steps: the loss, and the weights of the first and last layers and the
+        output layer against lr·steps, as c4_full2 at T = 64.
+    The measured errors are printed (pytest -s) for the record."""
+    print(f"gpu north star {name}", flush=True)
+    keep = kept_buffers(name)
+    rc, out, err, arrays = run_program(name, emulate=False, keep=keep, timeout=300)
+    assert rc == 0, err
+    z = vectors(name)
+    want_text = stdout_of(z)
+    want, got = _step1_loss(want_text), _step1_loss(out)
+    assert want is not None and got is not None, out
+    print(f"{name}: step-1 loss {got!r} vs {want!r}: rel {abs(got - want) / abs(want):.2e}", flush=True)
+    assert abs(got - want) <= 1e-4 * abs(want)
+    problem = outputs_match(want_text, out, rtol=1e-3)
+    assert problem is None, problem
+    steps = {"c2_full100": 100, "c4_t256_2": 2}.get(name)
+    for k in keep:
+        ref, val = z[f"buf:{k}"].astype(np.float64), arrays[k].astype(np.float64)
+        by_max = np.abs(val - ref) / np.abs(ref).max()
+        by_lr = np.abs(val - ref) / (1e-3 * steps)
+        print(f"  {k}: max {by_max.max():.2e} of max|w|; vs lr·steps max {by_lr.max():.3g}, "
+              f"p99 {np.percentile(by_lr, 99):.3g}", flush=True)
+        if name == "c2_full100" and k.endswith(".W"):
+            assert by_max.max() <= 1e-3, f"{k}: {by_max.max():.3g} of the largest weight"
+        else:
+            assert by_lr.max() <= 0.05 and np.percentile(by_lr, 99) <= (0.01 if name == "c2_full100" else 0.002), k
 
 
 @pytest.mark.parametrize("name", FUNCTIONS)
@@ -185,15 +223,14 @@ def test_gpu_failed_assert_exits_with_status_1():
 
 
 def test_gpu_checkpoint_save_then_load(tmp_path):
-    prog = patched_program("save_load", str(tmp_path), **{"/root/repo/tests/golden/programs/CKPT": str(tmp_path / "w.ckpt")})
-    rc1, out1, err1, _ = run_program(prog, emulate=False, timeout=120)
-    rc2, out2, err2, _ = run_program(prog, emulate=False, timeout=120)
+    rc1, out1, err1, _ = run_program("save_load", emulate=False, timeout=120, out_dir=tmp_path)
+    rc2, out2, err2, _ = run_program("save_load", emulate=False, timeout=120, out_dir=tmp_path)
     assert rc1 == 0 and rc2 == 0, err1 + err2
     assert out1.startswith("loaded 0.0000") and out2.startswith("loaded 1.0000")
     assert out1.split("sum")[1] == out2.split("sum")[1]
 
 
-@pytest.mark.parametrize("name", ["c2_small", "linreg", "c4_small"])
+@pytest.mark.parametrize("name", ["c2_small", "logreg", "c4_small"])
 def test_gpu_graph_replay_matches_reference(name):
     """The same programs with loop bodies captured once as HIP graphs and replayed."""
     print(f"gpu graphs {name}", flush=True)

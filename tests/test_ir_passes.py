@@ -129,7 +129,7 @@ def test_row_block_forwarding_reads_the_same_elements():
     makes as one vector for several outputs read consecutive, aligned elements (C2: W3's row j as
     5 8-byte loads)."""
     total = 0
-    for name in ["c2_wide_mlp", "c1_mlp", "c4_transformer", "c5_small", "mnist_like", "attention_train"]:
+    for name in ["c2_wide_mlp", "c1_mlp", "c4_transformer", "c5_small", "mnist_like", "attention_fit"]:
         for plan in row_block_plans(name):
             slots = {}
             for st in plan.stages:

@@ -12,16 +12,19 @@ import os
 import numpy as np
 import pytest
 
-from fixtures import load_ir, run_oracle, stdout_of, vector_names, vectors
+from fixtures import load_ir, load_ir_writing_to, run_oracle, stdin_of, stdout_of, vector_names, vectors, written_files
 from oracle import interp
 
 
 @pytest.mark.parametrize("name", vector_names(slow=os.environ.get("ANVIL_SLOW_ORACLE") == "1"))
-def test_oracle_matches_reference_interpreter(name):
-    prog, data = load_ir(name)
+def test_oracle_matches_reference_interpreter(name, tmp_path):
     z = vectors(name)
-    m, out = run_oracle(prog, data, z)
+    files = written_files(z)
+    prog, data = load_ir_writing_to(name, tmp_path) if files else load_ir(name)
+    m, out = run_oracle(prog, data, z, stdin=stdin_of(name))
     assert out == stdout_of(z)
+    for f in files:                                   # save_npy / save: the same bytes
+        assert (tmp_path / f).read_bytes() == bytes(z[f"file:{f}"]), f
     if "check_error" in z.files:                       # --check: the same element, tensor and message
         assert m.check_error == bytes(z["check_error"]).decode()
         return
