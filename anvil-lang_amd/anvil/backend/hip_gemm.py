@@ -26,8 +26,12 @@ from .hip_kernels import KernelScope, Plan, canon_key, decode
 
 MIN_WORK = 1 << 16           # M·N·K below which the generic schedules are as good
 MIN_SIDE = 32                # a narrower product (10 classes) wastes most of a 32-wide MFMA tile
-MIN_K = 16                   # a shorter sum (a 3 x 3 convolution of one input channel: K = 9) is a
-                             # memory-bound map: each lane sums its K terms itself
+MIN_K = 16                   # a shorter sum (a 3 x 3 convolution of one input channel: K = 9) is
+                             # memory-bound: OuterPlan, or a map where each lane sums its K terms
+OUTER_MAX_M = 64             # rows an OuterPlan lane runs in turn against its column
+OUTER_MIN_N = 4096           # columns (one lane each) that make an OuterPlan launch worth it
+OUTER_ROWS = 8               # rows per OuterPlan lane: more wavefronts in flight, and the row
+                             # operand's loads of a group issued together
 CUS = 256                    # compute units of an MI355X
 CU_WAVES = CUS * 4           # wavefronts that fill it once (one per SIMD)
 
@@ -276,9 +280,20 @@ def match(gen, k: ir.Kernel, name: str):
     if gen.emulate:
         return None
     s = analyse(k)
-    if s is None or not qualifies(s):
+    if s is None:
+        return None
+    if not qualifies(s):
+        if outer_ok(s):
+            return OuterPlan(gen, k, name, s)
         return None
     return GemmPlan(gen, k, name, s)
+
+
+def outer_ok(s) -> bool:
+    """A product with a sum too short for the matrix cores, few rows and many columns, plainly
+    addressed rows of A (what OuterPlan runs)."""
+    return (s.K < MIN_K and s.M <= OUTER_MAX_M and s.N >= OUTER_MIN_N and s.B == 1 and not s.k_multi
+            and not s.a_gather and not s.a_multi and os.environ.get("ANVIL_GEMM_OUTER", "1") != "0")
 
 
 def forward_gather_copies(prog: ir.Program, hosts: set) -> ir.Program:
@@ -539,7 +554,6 @@ class GemmPlan(Plan):
                 self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
             self.pipe = True
         self.forced = any(f.partition("@")[0] for f in os.environ.get("ANVIL_GEMM_FORCE", "").split(","))
-        self.stage = False              # the pipelined K split with k-contiguous operands staged in LDS
         self.followers = []             # (kernel, var map, forwarded loads) run in the epilogue
         self.layout()
 
@@ -578,21 +592,6 @@ class GemmPlan(Plan):
                 break
         nch = -(-(self.kslice // (8 * self.kgroup)) // self.waves)      # chunks per wave
         self.depth = max(1, min(int(os.environ.get("ANVIL_GEMM_DEPTH", "2" if nch <= 32 else "4")), nch))
-        # staging both operands through each wavefront's LDS (anvil_mm_tile_kstage) when both are
-        # contiguous in k (x·Wᵀ: an input gradient): one 32 x 32 tile per workgroup of four
-        # wavefronts, K in one range. Measured on 256 x 1024 x K products (one MI355X): 6.4 ns per
-        # k against 7.6 for the register-direct K split (C2's input gradient 10.9 -> 8.5-9.7 µs);
-        # with only A staged (x·W) it lost, 9.8 against 5.6 ns per k.
-        want = os.environ.get("ANVIL_GEMM_STAGE", "NT").split(",")
-        layout = {("ANVIL_LD_KC", "ANVIL_LD_RC"): "NN", ("ANVIL_LD_KC", "ANVIL_LD_KC"): "NT",
-                  ("ANVIL_LD_RC", "ANVIL_LD_RC"): "TN"}.get((self.amode, self.bmode))
-        self.stage = (self.pipe and self.waves == 4 and self.ptm * self.ptn == 1 and self.kslices == 1
-                      and layout is not None and (layout in want or layout + "s" in want)
-                      and not (s.k_multi or s.a_multi or s.b_multi) and s.K % 4 == 0
-                      and not (self.amode == "ANVIL_LD_RC" and s.a_gather)
-                      and not (self.bmode == "ANVIL_LD_RC" and s.b_gather))
-        # RC operands staged too ("NNs", "TNs"), or loaded straight into registers
-        self.stage_rc = layout is not None and layout + "s" in want
         # independent accumulator chains per wavefront when it has one 32 x 32 tile
         self.chains = int(os.environ.get("ANVIL_GEMM_CHAINS", "1")) if self.ptm * self.ptn == 1 else 1
         self.threads = 64 * self.waves if self.sched == "ksplit" else 256
@@ -655,9 +654,6 @@ class GemmPlan(Plan):
 
     def template_lds(self) -> int:
         """LDS of the anvil_mfma.h templates the kernel instantiates."""
-        if self.stage:
-            staged = 2 * (self.amode == "ANVIL_LD_KC" or self.stage_rc) + 2 * (self.bmode == "ANVIL_LD_KC" or self.stage_rc)
-            return 4 * 4 * max(staged * 32 * 36, 16 * 64)
         if self.slab:
             return 4 * (2 * 2 * self.slab * 33 + 4 * 16 * 64)
         if self.sched == "tile":
@@ -886,17 +882,6 @@ class GemmPlan(Plan):
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_kslab<{self.amode}, {self.bmode}, {self.slab}, {chk(s.M)}, {chk(s.N)}>"
                         f"(part, {kargs});"]
-            elif self.stage:
-                body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs, s.a_multi),
-                         self.row_fn(sc, "brow", s.b_gather, s.b_rs, s.b_multi)]
-                nch = -(-(-(-s.K // 32)) // 4)
-                depth = max(2, int(os.environ.get("ANVIL_GEMM_STAGE_DEPTH", "2")))
-                sa = "true" if self.stage_rc and self.amode == "ANVIL_LD_RC" else "false"
-                sb = "true" if self.stage_rc and self.bmode == "ANVIL_LD_RC" else "false"
-                main = ["    float part[1][1][4];",
-                        f"    anvil_mm_tile_kstage<{self.amode}, {self.bmode}, {nch}, {depth}, {chk(s.M)}, {chk(s.N)}, "
-                        f"{sa}, {sb}, {self.chains}>"
-                        f"(part, pa, arow, {s.a_ks}LL, pb, brow, {s.b_ks}LL, {s.M}, {s.N}, m0, n0, 0, {s.K}, opa, opb);"]
             elif self.pipe:
                 body += [self.row_fn(sc, "arow", s.a_gather, s.a_rs, s.a_multi),
                          self.row_fn(sc, "brow", s.b_gather, s.b_rs, s.b_multi),
@@ -920,7 +905,7 @@ class GemmPlan(Plan):
             value = "part[0][0][q]" if TM * TN == 1 else "part[ti][tj][q]"
         def head():                                   # after the body: its buffers are the parameters
             return [self.k_table("a") + self.k_table("b") + self.comment() + f" · {s.M}x{s.N}x{s.K}" + (f" x{s.B}" if s.B > 1 else "")
-                    + f" · {self.sched}{' staged' if self.stage else ''} {self.BM}x{self.BN}, A {self.amode[9:]}, "
+                    + f" · {self.sched} {self.BM}x{self.BN}, A {self.amode[9:]}, "
                     f"B {self.bmode[9:]}"
                     + (f" · K in {self.kslices} slices of {self.kslice}, partial tiles" if self.kslices > 1 else "")
                     + (f" · K over {len(s.k_multi)} variables" if s.k_multi else ""),
@@ -936,6 +921,78 @@ class GemmPlan(Plan):
             hoisted = self.hoistable([(k, None, [])] + list(self.followers))[:max(0, 64 // per)]
         pre, post = self.epilogue(sc, loop, slot, value, hoisted, per)
         return "\n".join(head() + body + pre + main + post + ["}"])
+
+
+class OuterPlan(GemmPlan):
+    """A product whose sum is too short for the matrix cores (K < MIN_K: C5's first convolution,
+    one input channel, K = 3 x 3) with few rows (M ≤ OUTER_MAX_M: its 32 output channels) and many
+    columns (N: its 128 x 26 x 26 output positions). One lane per column and group of OUTER_ROWS
+    rows (the grid's y): it loads the column's K operands of B into registers, then for each row of
+    its group sums the K products with that row of A in k order (the same addresses across the
+    wavefront: scalar loads, a group's issued together) and runs the epilogue, the followers
+    included. The column operand is read once per group and each result written once, a
+    wavefront's 64 stores of one row contiguous when the columns are the output's innermost index;
+    a row-per-lane map instead reloads the column's K operands for every row. (One lane per column
+    and all 32 rows left C5's 86528 columns 1352 wavefronts for 1024 SIMDs: 9.3 µs.)"""
+
+    def __init__(self, gen, k, name, spec: GemmSpec):
+        Plan.__init__(self, gen, [k], name)
+        self.k = k
+        self.s = spec
+        self.sched, self.BM, self.BN = "outer", spec.M, 1
+        self.kslices, self.kslice = 1, spec.K
+        self.waves, self.ptm, self.ptn = 4, 1, 1
+        self.threads = 256
+        self.forced = False
+        self.followers = []
+        self.rows = min(spec.M, int(os.environ.get("ANVIL_GEMM_OUTER_ROWS", OUTER_ROWS)))   # rows per lane
+        self.tm, self.tn = -(-spec.M // self.rows), -(-spec.N // self.threads)
+
+    def layout(self):
+        pass
+
+    def settle(self):
+        pass
+
+    def template_lds(self) -> int:
+        return 0
+
+    def grid(self):
+        return (self.tn, self.tm, 1), self.threads
+
+    def source(self) -> str:
+        s, k = self.s, self.k
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(k)
+        a_ptr = sc.buf(s.la.buf)
+        b_ptr = sc.buf(s.lb.buf)
+        body = [self.operand(sc, s.ea, s.la, "opa"), self.operand(sc, s.eb, s.lb, "opb"),
+                f"    const float *pa = {a_ptr} + ({s.la.offset.const});",
+                f"    const float *pb = {b_ptr} + ({s.lb.offset.const});",
+                self.row_fn(sc, "arow", None, s.a_rs),
+                self.row_fn(sc, "brow", s.b_gather, s.b_rs, s.b_multi),
+                self.k_fn("ak", "a"), self.k_fn("bk", "b"),
+                f"    const int ni = (int)(blockIdx.x * {self.threads}u + threadIdx.x);",
+                f"    if (ni >= {s.N}) return;",
+                f"    float bv[{s.K}];",
+                "    {",
+                "        const long long bo = brow(ni);",
+                "#pragma unroll",
+                f"        for (int kk = 0; kk < {s.K}; kk++) bv[kk] = opb(pb[bo + bk(kk)]);",
+                "    }"]
+        loop = ["#pragma unroll", f"    for (int r = 0; r < {self.rows}; r++) {{",
+                f"        const int mi = (int)blockIdx.y * {self.rows} + r;"]
+        if s.M % self.rows:
+            loop.append(f"        if (mi >= {s.M}) continue;")
+        loop += ["        const long long ao = arow(mi);",
+                "        float acc = 0.0f;",
+                "#pragma unroll",
+                f"        for (int kk = 0; kk < {s.K}; kk++) acc += opa(pa[ao + ak(kk)]) * bv[kk];"]
+        pre, post = self.epilogue(sc, loop, "0", "acc", [], 1)
+        head = [self.k_table("a") + self.k_table("b") + self.comment() + f" · {s.M}x{s.N}x{s.K} · outer: one lane "
+                f"per column and group of {self.rows} rows",
+                self.header(self.threads)]
+        return "\n".join(head + body + pre + post + ["}"])
 
 
 class GemmReducePlan(Plan):

@@ -446,186 +446,6 @@ __device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W]
             }
 }
 
-// The K split of anvil_mm_tile_kpipe (four wavefronts, one 32 x 32 tile, K in four shares) with the
-// operands that are contiguous in k staged through each wavefront's own LDS. Loading MFMA operands
-// straight into registers makes every load instruction touch 32 rows, one cache line each, of which
-// it uses 16-32 bytes: the texture path then moves a line per 16-32 useful bytes and is the bound
-// (measured on C2's batch-256 products: TA/TD busy ~80 %, the matrix cores ~30 %). Here a chunk
-// is 32 k: lane L of a wavefront loads 16 bytes at row L/8 + 8q (q = 0..3), k 4(L % 8): eight
-// lanes cover one row's 128 bytes, so an instruction touches 8 whole lines; the wavefront writes
-// the chunk to its LDS rows (row-major, 36 floats per row: the 16-byte writes and reads below are
-// free of bank conflicts) and reads it back in MFMA layout, lane (r, h) taking k = 16h .. 16h + 15
-// of row r, MFMA s pairing k = s with k = 16 + s. No barrier is needed: each wavefront owns its
-// LDS and a wavefront's LDS operations complete in order. An operand contiguous along its row
-// index (B of x·W, both operands of a weight gradient) is either staged the same way with k-rows
-// of 32 elements in LDS (SA / SB; read back one element per k) or loaded straight into registers,
-// where an instruction reads two whole lines of 32 elements.
-// D >= 2 chunks are in flight per wavefront, and two LDS slots per staged operand. The K range is
-// [kbeg, kbeg + K), K a multiple of 4; k past the end loads zeros. Rows (columns) past M (N) are
-// zero when CHKM (CHKN).
-template <int MODE, bool CHK, int D, bool STAGED>
-struct anvil_kstage_operand {
-    // staged: 4 x 16 bytes per lane and chunk; direct: 16 elements per lane and chunk
-    float r[D][16];
-    long long off[4];
-    bool ok[4];
-
-    // KC: the lane's four rows t0 + L/8 + 8q; RC staged: its four columns t0 + 4(L % 8) .. + 3, one
-    // offset (the columns are contiguous); RC direct: its column t0 + L % 32
-    template <class ROW>
-    __device__ __forceinline__ void rows(ROW row, int t0, int tmax, int lane) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int t = MODE == ANVIL_LD_KC ? t0 + (lane >> 3) + 8 * q : (STAGED ? t0 + 4 * (lane & 7) : t0 + (lane & 31));
-            ok[q] = !CHK || t < tmax;
-            off[q] = ok[q] ? row(t) : 0;
-        }
-    }
-
-    __device__ __forceinline__ void load(int d, const float *__restrict__ p, long long ks, int k0, int kend, int lane) {
-        if constexpr (MODE == ANVIL_LD_KC) {                     // 16 bytes of row (L/8 + 8q), k 4(L % 8)
-            const int k = k0 + 4 * (lane & 7);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                anvil_f32x4 v = {0.f, 0.f, 0.f, 0.f};
-                if (ok[q] && k < kend) v = *(const anvil_f32x4 *)(p + off[q] + k);
-                r[d][4 * q + 0] = v.x;
-                r[d][4 * q + 1] = v.y;
-                r[d][4 * q + 2] = v.z;
-                r[d][4 * q + 3] = v.w;
-            }
-        } else if constexpr (STAGED) {                           // 16 bytes of k-row (L/8 + 8q)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int k = k0 + (lane >> 3) + 8 * q;
-                anvil_f32x4 v = {0.f, 0.f, 0.f, 0.f};
-                if (ok[0] && k < kend) v = *(const anvil_f32x4 *)(p + off[0] + (long long)k * ks);
-                r[d][4 * q + 0] = v.x;
-                r[d][4 * q + 1] = v.y;
-                r[d][4 * q + 2] = v.z;
-                r[d][4 * q + 3] = v.w;
-            }
-        } else {                                                 // the lane's own MFMA operands
-            const int k = k0 + 16 * (lane >> 5);
-#pragma unroll
-            for (int s = 0; s < 16; s++)
-                r[d][s] = (ok[0] && k + s < kend) ? p[off[0] + (long long)(k + s) * ks] : 0.f;
-        }
-    }
-
-    // staged operands: the chunk in registers to the wavefront's LDS (KC: [t][k], RC: [k][t])
-    __device__ __forceinline__ void put(int d, float *__restrict__ lds, int lane) const {
-        if constexpr (MODE == ANVIL_LD_KC || STAGED) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const anvil_f32x4 v = {r[d][4 * q], r[d][4 * q + 1], r[d][4 * q + 2], r[d][4 * q + 3]};
-                *(anvil_f32x4 *)(lds + ((lane >> 3) + 8 * q) * 36 + 4 * (lane & 7)) = v;
-            }
-        }
-    }
-
-    // the lane's 16 MFMA operands of the chunk: row (column) L % 32, k = 16(L / 32) + s
-    __device__ __forceinline__ void get(int d, const float *__restrict__ lds, int lane, float (&f)[16]) const {
-        if constexpr (MODE == ANVIL_LD_KC) {
-            const float *row = lds + (lane & 31) * 36 + 16 * (lane >> 5);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const anvil_f32x4 v = *(const anvil_f32x4 *)(row + 4 * j);
-                f[4 * j] = v.x;
-                f[4 * j + 1] = v.y;
-                f[4 * j + 2] = v.z;
-                f[4 * j + 3] = v.w;
-            }
-        } else if constexpr (STAGED) {
-            const float *col = lds + 16 * (lane >> 5) * 36 + (lane & 31);
-#pragma unroll
-            for (int s = 0; s < 16; s++) f[s] = col[s * 36];
-        } else {
-#pragma unroll
-            for (int s = 0; s < 16; s++) f[s] = r[d][s];
-        }
-    }
-};
-
-template <int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, bool SA, bool SB, int CH, class AROW,
-          class BROW, class OPA, class OPB>
-__device__ __forceinline__ void anvil_mm_tile_kstage(float (&out)[1][1][4],
-                                                     const float *__restrict__ a, AROW arow, long long a_ks,
-                                                     const float *__restrict__ b, BROW brow, long long b_ks,
-                                                     int M, int N, int m0, int n0, int kbeg, int K, OPA opa, OPB opb) {
-    static_assert(D >= 2, "a chunk is put into LDS while the next ones are loading");
-    constexpr int STAGE = 32 * 36;                      // floats of one staged chunk
-    constexpr int NA = (AMODE == ANVIL_LD_KC || SA) ? 2 : 0, NB = (BMODE == ANVIL_LD_KC || SB) ? 2 : 0;
-    __shared__ float stage[4][(NA + NB) * STAGE > 16 * 64 ? (NA + NB) * STAGE : 16 * 64];
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int kend = kbeg + K, c0 = w * NCH;
-    const int n = min(NCH, max(0, (K + 31) / 32 - c0));           // this wavefront's chunks
-    float *as = stage[w], *bs = stage[w] + NA * STAGE;
-    anvil_kstage_operand<AMODE, CHKM, D, SA> oa;
-    anvil_kstage_operand<BMODE, CHKN, D, SB> ob;
-    oa.rows(arow, m0, M, lane);
-    ob.rows(brow, n0, N, lane);
-    anvil_mm_acc<1, 1> acc, acc2;
-    acc.zero();
-    if (CH > 1) acc2.zero();
-    // Chunk c: loaded into register set c % D, put into LDS slot c % 2 and read back into operand
-    // set c % 2 during chunk c - 1's products, so the LDS round trip overlaps the matrix cores.
-    float fa[2][16], fb[2][16];
-#pragma unroll
-    for (int c = 0; c < D; c++) {
-        if (c < n) {
-            oa.load(c, a, a_ks, kbeg + 32 * (c0 + c), kend, lane);
-            ob.load(c, b, b_ks, kbeg + 32 * (c0 + c), kend, lane);
-        }
-    }
-    if (n > 0) {
-        oa.put(0, as, lane);
-        ob.put(0, bs, lane);
-        oa.get(0, as, lane, fa[0]);
-        ob.get(0, bs, lane, fb[0]);
-    }
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        if (c < n) {
-            if (c + 1 < n) {
-                oa.put((c + 1) % D, as + ((c + 1) % 2) * STAGE, lane);
-                ob.put((c + 1) % D, bs + ((c + 1) % 2) * STAGE, lane);
-                oa.get((c + 1) % D, as + ((c + 1) % 2) * STAGE, lane, fa[(c + 1) % 2]);
-                ob.get((c + 1) % D, bs + ((c + 1) % 2) * STAGE, lane, fb[(c + 1) % 2]);
-            }
-            if (c + D < n) {                                        // set c % D was put last iteration
-                oa.load(c % D, a, a_ks, kbeg + 32 * (c0 + c + D), kend, lane);
-                ob.load(c % D, b, b_ks, kbeg + 32 * (c0 + c + D), kend, lane);
-            }
-#pragma unroll
-            for (int s = 0; s < 16; s++) {
-                if (CH > 1 && (s & 1))
-                    acc2.c[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(opa(fa[c % 2][s]), opb(fb[c % 2][s]),
-                                                                        acc2.c[0][0], 0, 0, 0);
-                else
-                    acc.c[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(opa(fa[c % 2][s]), opb(fb[c % 2][s]),
-                                                                       acc.c[0][0], 0, 0, 0);
-            }
-        }
-    }
-    if (CH > 1) acc.c[0][0] += acc2.c[0][0];
-    // the four partial tiles, added through LDS in wave order (each wavefront overwrites only its own
-    // staging rows, which it alone has read)
-    float *part = &stage[0][0];
-    constexpr int ROW = sizeof(stage[0]) / sizeof(float);
-#pragma unroll
-    for (int v = 0; v < 16; v++) stage[w][v * 64 + lane] = acc.c[0][0][v];
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        float sum = 0.f;
-#pragma unroll
-        for (int src = 0; src < 4; src++) sum += part[src * ROW + (4 * w + q) * 64 + lane];
-        out[0][0][q] = sum;
-    }
-}
-
 // The K split with operands staged through LDS: the workgroup's 256 lanes load each KC-deep chunk
 // of A (32 rows) and B (32 columns) with 16-byte loads along whichever index is contiguous in
 // memory (a wavefront's load covers a few whole cache lines, where loading MFMA operands straight

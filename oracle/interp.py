@@ -202,13 +202,20 @@ class Machine:
     """Runs an `ir.Program` (this package's IR, or anything with the same shape) on the CPU.
 
     float_dtype: np.float32 for the reference semantics (np.float64 for gradient checks).
+    sum_order: "numpy" (the reference's: NumPy's own float sums) for every parity check; "reversed"
+    (each float sum over its reduction variables taken from the last element to the first) or
+    "sequential" (one running float sum, in index order) measure how far the same algorithm moves
+    when only the order of its additions changes (tests/golden/make_noise_floor.py).
     loop_hook(counter_name, value): called before each iteration of every `for` loop; it may raise
     StopRun to end the run (the CPU baseline times a bounded sample this way).
     """
 
     def __init__(self, prog, out=None, seed: int = 0, inp=None, float_dtype=np.float32, loop_hook=None,
-                 check=None):
+                 check=None, sum_order="numpy"):
+        if sum_order not in ("numpy", "reversed", "sequential"):
+            raise ValueError(f"sum_order {sum_order!r}")
         self.prog = prog
+        self.sum_order = sum_order
         self.check = check                # "nan" | "inf": stop at the first nan (or infinity) a kernel makes
         self.out = out if out is not None else sys.stdout
         self.inp = inp if inp is not None else sys.stdin
@@ -543,11 +550,18 @@ class Machine:
             else:
                 a[off.reshape(-1)] = val.reshape(-1)
 
-    @staticmethod
-    def reduce(op, body, nd):
+    def reduce(self, op, body, nd):
         axes = tuple(range(nd, body.ndim))
         if op == "sum":
-            return body.sum(axis=axes, dtype=body.dtype)
+            if self.sum_order == "numpy" or body.dtype.kind != "f" or not axes:
+                return body.sum(axis=axes, dtype=body.dtype)
+            flat = body.reshape(body.shape[:nd] + (-1,))
+            if self.sum_order == "reversed":
+                return flat[..., ::-1].sum(axis=-1, dtype=body.dtype)
+            acc = np.zeros(flat.shape[:-1], body.dtype)
+            for i in range(flat.shape[-1]):
+                acc += flat[..., i]
+            return acc
         if op == "prod":
             return body.prod(axis=axes, dtype=body.dtype)
         if op == "max":

@@ -576,6 +576,9 @@ PROGRAMS = [
     # against float64 closed forms)
     {"name": "c3_linear_mid", "source": C3_LINEAR,
      "function": {"name": "linear", "args": [([4096, 256], "f32"), ([1024, 256], "f32"), ([1024], "f32")]}},
+    # C2's layer shape as x·Wᵀ (both operands contiguous in k, as in C2's input gradient)
+    {"name": "c3_linear_b256", "source": C3_LINEAR,
+     "function": {"name": "linear", "args": [([256, 1024], "f32"), ([1024, 1024], "f32"), ([1024], "f32")]}},
     {"name": "c3_bmm", "source": C3_BMM,
      "function": {"name": "bmm", "args": [([64, 256, 64], "f32"), ([64, 64, 256], "f32")]}},
     {"name": "c3_attention", "source": C3_ATTENTION,

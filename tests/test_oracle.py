@@ -146,14 +146,46 @@ def test_oracle_catches_a_planted_mistake():
     z = vectors("c3_softmax_small")
 
     class Broken(interp.Machine):
-        @staticmethod
-        def reduce(op, body, nd):
+        def reduce(self, op, body, nd):
             if op == "sum":
                 body = body[..., :-1]
-            return interp.Machine.reduce(op, body, nd)
+            return super().reduce(op, body, nd)
     m = Broken(prog, out=io.StringIO())
     by_id = {b.id: b for b in prog.buffers}
     m.arr(by_id[data["function"]["inputs"][0]])[:] = z["input0"].reshape(-1)
     m.run()
     b = by_id[data["function"]["outputs"][0]]
     assert not np.array_equal(m.arr(b)[:b.numel].reshape(b.shape), z["output0"])
+
+
+def _linear_with_order(order):
+    prog, data = load_ir("c3_linear_small")
+    z = vectors("c3_linear_small")
+    m = interp.Machine(prog, out=io.StringIO(), sum_order=order)
+    by_id = {b.id: b for b in prog.buffers}
+    for k, bid in enumerate(data["function"]["inputs"]):
+        m.arr(by_id[bid])[:] = z[f"input{k}"].reshape(-1)
+    m.run()
+    b = by_id[data["function"]["outputs"][0]]
+    return m.arr(b)[:b.numel].reshape(b.shape).copy(), z
+
+
+def test_reordered_sums_change_only_the_rounding():
+    """The oracle's other summation orders (used to measure the reorder spread of trained weights,
+    tests/golden/make_noise_floor.py): the same sums up to float32 rounding, against float64 NumPy,
+    and really another order (some results differ from NumPy's in the last bits); the reversed and
+    sequential sums of 1, 2**-24, 2**-24 have closed forms (2**-24 is half an ulp of 1)."""
+    x, w, bias = (vectors("c3_linear_small")[f"input{k}"].astype(np.float64) for k in range(3))
+    exact = x @ w.T + bias
+    base, _ = _linear_with_order("numpy")
+    for order in ("reversed", "sequential"):
+        got, _ = _linear_with_order(order)
+        np.testing.assert_allclose(got, exact, rtol=0, atol=1e-5 * np.abs(exact).max())
+        assert not np.array_equal(got, base), order
+    body = np.array([[1.0, 2.0 ** -24, 2.0 ** -24]], np.float32)
+    m = interp.Machine(load_ir("c3_linear_small")[0], out=io.StringIO(), sum_order="sequential")
+    assert m.reduce("sum", body, 1)[0] == np.float32(1.0)             # 1 + h rounds to 1, twice
+    m.sum_order = "reversed"
+    assert m.reduce("sum", body, 1)[0] == np.float32(1.0 + 2.0 ** -23)  # h + h = ulp(1), then exact
+    with pytest.raises(ValueError):
+        interp.Machine(load_ir("c3_linear_small")[0], sum_order="pairwise")
