@@ -665,4 +665,8 @@ PROGRAMS = [
     {"name": "c4_t256_2", "source": C4, "consts": {"STEPS": 2, "T": 256}, "interp": True,
      "keep": ["net.layers.0.Wqkv", "net.layers.3.ff_in.W", "net.head.W", "net.head.b"]},
     {"name": "c5_step1", "source": C5, "consts": {"STEPS": 1}, "interp": True},
+    # C5's first convolution with 12 output channels: the outer-product schedule's row groups of 8
+    # end in a partial group of 4
+    {"name": "c5_conv12", "source": C5, "consts": {"STEPS": 2, "NB": 32, "C1": 12, "C2": 16, "HID": 32},
+     "interp": True, "keep": ["net.c1.W", "net.c1.b", "net.c2.W", "net.fc1.W"]},
 ]
