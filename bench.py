@@ -25,6 +25,7 @@ import argparse
 import ctypes
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -237,14 +238,22 @@ def host_description() -> str:
     return f"{model}, {os.cpu_count()} logical CPUs; environment {env}"
 
 
-def oracle_run(prog, data, counter: str, stop_after: int | None):
-    """The NumPy interpreter (oracle/interp.py) on an IR program with every BLAS/OpenMP pool limited
-    to one thread: the perf_counter time at each start of the `counter` loop's iterations, and at
-    the end of the run (or when stop_after iterations have started)."""
+ONE_THREAD = {"OMP_NUM_THREADS": "1", "OPENBLAS_NUM_THREADS": "1", "MKL_NUM_THREADS": "1"}
+
+
+def oracle_leg(path: str, counter: str, stop_after: int | None) -> dict:
+    """Run in a child process started with ONE_THREAD in its environment: the NumPy interpreter
+    (oracle/interp.py) on the IR program at `path`, every BLAS/OpenMP pool also limited to one
+    thread at run time; the perf_counter time at each start of the `counter` loop's iterations and
+    at the end of the run (or when stop_after iterations have started), and the host's description."""
     import io
     sys.path.insert(0, ROOT)
     from threadpoolctl import threadpool_limits
+    from anvil import irjson
     from oracle import interp
+    with open(path) as f:
+        data = json.load(f)
+    prog = irjson.load(data)
     marks = []
 
     def hook(name, value):
@@ -258,17 +267,30 @@ def oracle_run(prog, data, counter: str, stop_after: int | None):
             m.run()
         except interp.StopRun:
             pass
-    return marks, time.perf_counter()
+    end = time.perf_counter()
+    return {"marks": [t - marks[0] for t in marks], "end": end - marks[0], "host": host_description()}
 
 
-def cpu_baseline(prog, data, steps: int):
+def oracle_run(path: str, counter: str, stop_after: int | None) -> dict:
+    """oracle_leg in a child process whose environment pins BLAS and OpenMP to one thread (the child
+    touches no GPU)."""
+    cmd = [sys.executable, os.path.abspath(__file__), "--oracle-leg", path, counter, str(stop_after or 0)]
+    r = subprocess.run(cmd, capture_output=True, text=True, env=dict(os.environ, **ONE_THREAD))
+    if r.returncode != 0:
+        raise SystemExit(f"bench: the CPU baseline failed:\n{r.stderr[-2000:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def cpu_baseline(steps: int):
     """The NumPy interpreter on the same IR: set-up untimed, one warm-up step, then `steps` steps."""
-    marks, _ = oracle_run(prog, data, LOOP_COUNTER, steps + 1)
+    run = oracle_run(WORKLOAD, LOOP_COUNTER, steps + 1)
+    marks = run["marks"]
     t = marks[-1] - marks[1]
     return {"value": round(steps * BATCH / t, 2), "unit": "samples/s", "cores": 1, "kind": "port",
             "sample": f"{steps} full-size C2 training steps (batch 256) after 1 warm-up step, NumPy "
-                      f"interpreter (oracle/interp.py) with every BLAS/OpenMP thread pool limited to 1 "
-                      f"(threadpoolctl); host: {host_description()}; {t:.1f} s"}
+                      f"interpreter (oracle/interp.py) in a child process with OMP_NUM_THREADS = "
+                      f"OPENBLAS_NUM_THREADS = MKL_NUM_THREADS = 1 (and every thread pool limited to 1 "
+                      f"at run time, threadpoolctl); host: {run['host']}; {t:.1f} s"}
 
 
 C1_WORKLOAD = os.path.join(ROOT, "tests", "golden", "ir", "c1_mlp.json")
@@ -300,12 +322,14 @@ def c1_epoch(cpu: bool) -> dict:
     out = {"steps": n, "gpu_samples_per_s": gpu, "gpu_epoch_ms_steps": round(ms * n / (n - 1), 3),
            "gpu_program_wall_s": round(wall, 3), "library": os.path.basename(lib.path)}
     if cpu:
-        marks, end = oracle_run(prog, data, LOOP_COUNTER, None)
+        run = oracle_run(C1_WORKLOAD, LOOP_COUNTER, None)
+        marks = run["marks"]
         steps = len(marks)
         t_steps = marks[-1] - marks[0]
         out.update({"cpu_samples_per_s": round((steps - 1) * C1_BATCH / t_steps, 1),
-                    "cpu_epoch_s": round(end - marks[0], 2),
-                    "cpu": f"oracle/interp.py, one thread (threadpoolctl); {host_description()}",
+                    "cpu_epoch_s": round(run["end"], 2),
+                    "cpu": f"oracle/interp.py in a child process with OMP_NUM_THREADS = OPENBLAS_NUM_THREADS = "
+                           f"MKL_NUM_THREADS = 1 (and threadpoolctl); {run['host']}",
                     "speedup": round(gpu / ((steps - 1) * C1_BATCH / t_steps), 1)})
     return out
 
@@ -345,7 +369,7 @@ def main() -> int:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=480)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--cpu-steps", type=int, default=3)
+    p.add_argument("--cpu-steps", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-c1", action="store_true", help="skip config C1's one-epoch run (GPU and CPU)")
     p.add_argument("--profile-table", action="store_true", help="print every kernel's time to stderr")
@@ -353,7 +377,12 @@ def main() -> int:
     p.add_argument("--copy", action="store_true", help="run the copy kernel that calibrates HBM counters")
     p.add_argument("--c3", action="store_true", help="config C3: the standalone functions, per kernel")
     p.add_argument("--yardstick", action="store_true", help="torch.mm (the vendor library) on C2's product shapes")
+    p.add_argument("--oracle-leg", nargs=3, metavar=("IR", "COUNTER", "STOP"), help=argparse.SUPPRESS)
     args = p.parse_args()
+    if args.oracle_leg:
+        path, counter, stop = args.oracle_leg
+        print(json.dumps(oracle_leg(path, counter, int(stop) or None)), flush=True)
+        return 0
     if args.yardstick:
         print(json.dumps(yardstick()), flush=True)
         return 0
@@ -390,7 +419,7 @@ def main() -> int:
         "step_roofline": step_roofline(prof, ms / args.steps),
     }
     if not args.no_cpu:
-        cpu = cpu_baseline(prog, data, args.cpu_steps)
+        cpu = cpu_baseline(args.cpu_steps)
         line["cpu_baseline"] = cpu
         line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
     if not args.no_c1:
