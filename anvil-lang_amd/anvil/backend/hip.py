@@ -264,7 +264,8 @@ class HipGen:
         k = stmts[i].kernel
         if not k.domain or not 64 <= k.domain[0].extent <= 4096:
             return None
-        rb = HK.RowBlockBuilder(k.domain[0].extent)
+        prior = {b.id for st in stmts[:i] if isinstance(st, KernelStmt) for b in A.kernel_writes(st.kernel)}
+        rb = HK.RowBlockBuilder(k.domain[0].extent, prior)
         j = i
         while j < len(stmts) and isinstance(stmts[j], KernelStmt) and rb.fits(stmts[j].kernel, self.hosts):
             j += 1

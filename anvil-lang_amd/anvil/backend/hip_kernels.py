@@ -921,12 +921,15 @@ class RowBlockBuilder:
 
     MAX_ROW_WORK = 1 << 15          # outputs x reduction length per row and stage
 
-    def __init__(self, R: int):
+    MIN_ROW_FOR_PRIOR = 128         # see `prior` below
+
+    def __init__(self, R: int, prior: set = frozenset()):
         self.R = R
         self.kernels: list = []
         self.written: dict = {}     # buffer id -> row slice
         self.far: set = set()       # buffers some stage reads outside its row
         self.before: set = set()    # buffers read before the chain writes them (their old values)
+        self.prior = prior          # buffers an earlier kernel of the same block wrote
 
     def slice_of(self, b):
         n = b.root.numel
@@ -943,13 +946,19 @@ class RowBlockBuilder:
             return False
         # a buffer whose old contents a stage reads is not written by the chain: the chain's
         # launch is one position of the program for the arena, where the reads of buffers the
-        # launch writes are taken to be of the launch's own values
+        # launch writes are taken to be of the launch's own values. Unless an earlier kernel of the
+        # same block wrote it: its lifetime then began before the launch (a gradient a product
+        # wrote and a stage adds to, layer norm's input gradient). That is taken only for rows of
+        # MIN_ROW_FOR_PRIOR elements or more: a workgroup per row of 64 (C4's softmax gradient at
+        # T = 64, 4096 rows) measured 17.8 µs against 7.8 for its three launches.
         before = self.before | {b.id for b in A.kernel_reads(k) if b.id not in self.written}
         written = dict(self.written)
+        long_rows = E >= self.MIN_ROW_FOR_PRIOR
         for st in k.stores:
             b = st.buf.root
             S = self.slice_of(b)
-            if b.id in self.far or b.id in before or not row_local(st.offset, k, self.R, S):
+            if (b.id in self.far or (b.id in before and not (long_rows and b.id in self.prior))
+                    or not row_local(st.offset, k, self.R, S)):
                 return False
             written[b.id] = S
         far = set()
