@@ -51,8 +51,9 @@ class HipToolchainError(Exception):
     pass
 
 
-def runtime_source() -> str:
-    """anvil_rt.h and anvil_hip.h (and the MFMA templates), inlined: a generated file stands alone."""
+def runtime_source(attn_train: bool = False) -> str:
+    """anvil_rt.h and anvil_hip.h (and the MFMA templates; the training attention's when a plan uses
+    them), inlined: a generated file stands alone."""
     def read(name):
         with open(os.path.join(RUNTIME_DIR, name)) as f:
             return f.read().replace("#pragma once\n", "")
@@ -62,6 +63,8 @@ def runtime_source() -> str:
     if os.path.exists(gemm_path):
         bk = os.environ.get("ANVIL_GEMM_TILE_BK")
         dev += "\n" + (f"#define ANVIL_MM_BK {int(bk)}\n" if bk else "") + read("anvil_mfma.h")
+        if attn_train:
+            dev += "\n" + read("anvil_attn_train.h")
     return dev
 
 
@@ -128,6 +131,7 @@ class HipGen:
         self.emulate = emulate
         self.hosts = A.host_scalars(prog)
         self.readers = A.all_readers(prog)
+        self.attn_train: dict = {}          # first kernel id -> (plan, statements) of a training-attention chain
         self.graphs = graphs
         self.dev_hosts = self.device_visible_hosts() if graphs else set()
         self.hsd = {bid: i for i, bid in enumerate(sorted(self.dev_hosts))}
@@ -246,10 +250,13 @@ class HipGen:
         if self.check:
             return self.plan_one(stmts, i)
         if not self.emulate and os.environ.get("ANVIL_HIP_ATTN", "1") != "0":
-            from . import hip_attn
+            from . import hip_attn, hip_attn_train
             at = hip_attn.match(self, stmts, i)
             if at is not None:
                 return at, 6
+            got = hip_attn_train.match(self, stmts, i)
+            if got is not None:
+                return got
         from . import hip_conv
         got = hip_conv.match_dgrad(self, stmts, i) or self.row_block(stmts, i)
         if got is not None:
@@ -344,7 +351,7 @@ class HipGen:
         The scan may cross one `if (host scalar) break;` (a step limit checked after the batch is
         gathered): the launch then goes after the check, and the leaving path launches the parts
         that came before the check on their own, so they run exactly when they did."""
-        if self.emulate or self.check or os.environ.get("ANVIL_HIP_SIDE", "1") == "0":
+        if self.emulate or self.check or os.environ.get("ANVIL_HIP_SIDE", "1") == "0" or getattr(plan, "alone", False):
             return plan, used
         ids = lambda bs: {b.root.id for b in bs}
 
@@ -378,7 +385,7 @@ class HipGen:
                 j += 1
                 continue
             cand, cused = self.plan_run(stmts, j)
-            if cand.kind in ("serial", "fused"):
+            if cand.kind in ("serial", "fused") or getattr(cand, "alone", False):
                 break
             if getattr(cand, "kslices", 1) > 1 and exit_at is not None:
                 break                                   # its second launch follows the fused one
@@ -567,7 +574,8 @@ class HipGen:
                         if twin is not None:
                             seg.append(("twin", self.launch(twin, ind), twin))
                 seg.append(("launch", self.launch(plan, ind), plan))
-                if getattr(plan, "kslices", 1) > 1:           # a K split across workgroups: its sum
+                if getattr(plan, "kslices", 1) > 1 or getattr(plan, "two_launches", False):
+                    # a K split across workgroups: its sum; or the plan's own second launch
                     if not hasattr(plan, "reduce_plan"):
                         plan.reduce_plan = plan.second()
                         self.plans.append(plan.reduce_plan)
@@ -884,17 +892,20 @@ class HipGen:
                                                 "scratch")
         dev = sorted(self.device_bufs.values(), key=lambda b: b.id)
         share = os.environ.get("ANVIL_HIP_SHARE", "1") != "0"
-        plan = A.plan_arena(self.prog, dev, self.full_writer, share=share, fused=self.fused_group)
+        plan = A.plan_arena(self.prog, dev, self.full_writer, share=share, fused=self.fused_group,
+                            extra=self.extra_reads)
+        self.arena = plan
         # the no-allocation entry: the caller brings the arguments and results, so its scratch
         # holds only the other buffers (same lifetime sharing)
         extern_ids = {b.id for b in externs}
         inner = [b for b in dev if b.id not in extern_ids]
-        splan = A.plan_arena(self.prog, inner, self.full_writer, share=share, fused=self.fused_group)
+        splan = A.plan_arena(self.prog, inner, self.full_writer, share=share, fused=self.fused_group,
+                             extra=self.extra_reads)
         src = self.prog.source
         name = src.display_path() if src is not None and hasattr(src, "display_path") else "<program>"
         out = [f"// Generated by anvil (HIP backend) from {name} for MI355X ({ARCH}).",
                f"// Build: hipcc --offload-arch={ARCH} {' '.join(f for f in HIP_FLAGS if f != '-w')} prog.hip -o prog.so -lz",
-               "", runtime_source(), "",
+               "", runtime_source(any(p.kind.startswith("attention-train") for p in self.plans)), "",
                "// ---------------------------------------------------------------- buffers"]
         for b in dev:
             where = f"arena + {plan.offsets[b.id]}"
@@ -1080,12 +1091,23 @@ class HipGen:
             part._writes = part.writes()
         return id(plan), part._writes
 
+    def extra_reads(self, st) -> set:
+        """Buffers a launch reads beyond the IR kernels it replaces (noted at its first kernel)."""
+        if not isinstance(st, KernelStmt):
+            return set()
+        plan = self.group_of.get(st.kernel.id)
+        if plan is None or not plan.kernels or plan.kernels[0] is not st.kernel or not hasattr(plan, "extra_reads"):
+            return set()
+        return plan.extra_reads()
+
     def full_writer(self, st, b) -> bool:
         if isinstance(st, KernelStmt):
             plan = self.plan_of.get(st.kernel.id)
             k = st.kernel
             if plan is not None:
                 plan = plan[0]
+                if hasattr(plan, "full_writes"):
+                    return b.id in plan.full_writes()
                 if any((k.id, i) in plan.skip_stores for i, s in enumerate(k.stmts)
                        if isinstance(s, ir.Store) and s.buf.root is b):
                     return False

@@ -386,6 +386,7 @@ class ArenaPlan:
     size: int = 0
     shared_bytes: int = 0                            # what the shared buffers would take apart
     placed_bytes: int = 0
+    spans: dict = field(default_factory=dict)       # buffer id -> (first, last) program position, if shared
 
 
 def _full_write(k: ir.Kernel, b: Buffer) -> bool:
@@ -404,11 +405,14 @@ def _full_write(k: ir.Kernel, b: Buffer) -> bool:
     return False
 
 
-def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = True, fused=None) -> ArenaPlan:
+def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = True, fused=None,
+               extra=None) -> ArenaPlan:
     """Offsets for device_bufs. full_writer(stmt, buf) says whether a statement writes all of buf.
     fused(kernel) -> (group key, buffers the group writes) or None: the kernels of one generated
     kernel run together, so they are one position of the program (reads of what the group itself
     writes are of the lane's own elements and do not start a lifetime early).
+    extra(stmt) -> buffers the statement's launch reads beyond its IR kernel (a fused chain that
+    reads a buffer the IR's own kernels had finished with): they stay live up to it.
     share=False gives every buffer its own bytes ($ANVIL_HIP_SHARE=0: for inspecting temporaries)."""
     uses: dict[int, list] = {}
     loops: list[tuple[int, int]] = []
@@ -461,7 +465,7 @@ def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = T
             if group is not None:
                 key, own = group
                 here[0] = group_pos.setdefault(key, pos)    # every part of one launch: one position
-            for b in stmt_reads(st):
+            for b in stmt_reads(st) | (extra(st) if extra is not None else set()):
                 if b not in own:
                     note(b, chain)
             for b in stmt_writes(st):
@@ -519,6 +523,7 @@ def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = T
             o = max(o, e)
         placed.append((lo, hi, o, n))
         plan.offsets[b.id] = base + o
+        plan.spans[b.id] = (lo, hi)
         top = max(top, o + n)
     plan.shared_bytes = sum(n for _, _, n in shared)
     plan.placed_bytes = top

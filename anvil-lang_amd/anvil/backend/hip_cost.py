@@ -74,6 +74,8 @@ def plan_cost(plan) -> tuple[int, int]:
     """(FLOPs, bytes) of one launch of a generated kernel. A matrix product counts 2·M·N·K (per batch)
     for its contraction, the matrix-core work, whatever scale factors the IR multiplies inside the
     sum (they are applied once per output); launches of several kernels side by side add up."""
+    if hasattr(plan, "cost"):                           # a plan that knows its own work
+        return plan.cost()
     if plan.kind == "fused":
         fl = by = 0
         for p in plan.parts:

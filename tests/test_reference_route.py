@@ -36,7 +36,8 @@ def test_ir_constructors_take_the_reference_arguments():
     from anvil import ir
     assert list(inspect.signature(ir.Buffer).parameters) == ["name", "shape", "dtype", "kind", "init", "span"]
     assert list(inspect.signature(ir.Var).parameters) == ["name", "extent"]
-    for mod in ("hip", "hip_analysis", "hip_attn", "hip_conv", "hip_cost", "hip_emit", "hip_gemm", "hip_kernels"):
+    for mod in ("hip", "hip_analysis", "hip_attn", "hip_attn_train", "hip_conv", "hip_cost", "hip_emit", "hip_gemm",
+                "hip_kernels"):
         path = os.path.join(os.path.dirname(ir.__file__), "backend", f"{mod}.py")
         with open(path) as f:
             text = f.read()
