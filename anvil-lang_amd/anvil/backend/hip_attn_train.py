@@ -449,6 +449,7 @@ def _backward(gen, stmts: list, j: int, sh: _Shape):
     if sh.L in A.kernel_writes(k3) or dO is G or any(gen.is_host(b) for b in (sh.QKV, sh.O, dO, G)):
         return None
     sh.G, sh.dO = G, dO
+    sh.DL = DL                          # [B·H·T]: holds Drow between the two backward launches
     return kernels
 
 
@@ -544,11 +545,11 @@ class _AttnTrainPlan(Plan):
                  f"    a.m = {m}; a.l = {l};",
                  f"    a.H = {sh.H}; a.BH = {sh.B * sh.H}; a.alpha = {flit(sh.alpha)};"]
         if backward:
-            g, do = self.use_buf(sh.G), self.use_buf(sh.dO)
-            lines += [f"    a.dout = {do} + {sh.o0}LL;",
+            g, do, dr = self.use_buf(sh.G), self.use_buf(sh.dO), self.use_buf(sh.DL)
+            lines += [f"    a.dout = {do} + {sh.o0}LL; a.drow = {dr};",
                       f"    a.dq = {g} + {sh.q0}LL; a.dk = {g} + {sh.k0}LL; a.dv = {g} + {sh.v0}LL;"]
         else:
-            lines += ["    a.dout = nullptr; a.dq = a.dk = a.dv = nullptr;"]
+            lines += ["    a.dout = nullptr; a.drow = nullptr; a.dq = a.dk = a.dv = nullptr;"]
         return lines
 
     def units(self) -> int:
@@ -590,10 +591,10 @@ class AttnTrainBwdPlan(_AttnTrainPlan):
     two_launches = True
 
     def writes(self) -> set:
-        return {self.sh.G}
+        return {self.sh.G, self.sh.DL}
 
     def full_writes(self) -> set:
-        return {self.sh.G.id}
+        return {self.sh.G.id, self.sh.DL.id}
 
     def extra_reads(self) -> set:
         """What the launches read beyond the IR kernels they replace: the forward's row maxima and

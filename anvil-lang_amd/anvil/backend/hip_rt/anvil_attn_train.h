@@ -27,8 +27,8 @@
 // the other operand in column form (row 8(e/4) + 4h + e%4, feature D/32·r + j for output tile j).
 //
 // Three launches: the forward writes O and the row statistics m₂ and l; the backward's dQ launch
-// (query-tile pairs, K and V staged) and dK/dV launch (key-tile pairs, Q and dO staged) each
-// recompute P from Q, K, m₂ and l.
+// (query tiles, K and V staged; it also writes Drow) and dK/dV launch (key tiles: their own K and V
+// rows in LDS, Q, dO and the row statistics staged) each recompute P from Q, K, m₂ and l.
 #pragma once
 #ifndef ANVIL_EMULATE
 
@@ -39,6 +39,7 @@ struct anvil_attn_io {
     const float *dout;               //   element (n, h, t, c) at n·on + h·oh + t·os + c
     long long on, oh, os;
     float *m, *l;                    // row statistics: element (n, h, t) at (n·H + h)·T + t
+    float *drow;                     // Drow, in the row statistics' layout (dQ launch → dK/dV launch)
     float *dq, *dk, *dv;             // gradients, in Q's layout
     int H, BH;                       // heads, and batch × heads
     float alpha;
@@ -190,6 +191,11 @@ __device__ __forceinline__ void anvil_attn_fwd(const anvil_attn_io &a) {
 #pragma unroll
                 for (int x = 0; x < 4; x++) st = __builtin_amdgcn_mfma_f32_32x32x2f32(kx[x], qr[c][x], st, 0, 0, 0);
             }
+            // the V operands of P·V, read now: their LDS latency passes under the softmax
+            vec vx[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) vx[e] = *(const vec *)&vs[(8 * (e >> 2) + 4 * h + (e & 3)) * P + DT * r];
+            __builtin_amdgcn_sched_barrier(0);
             if (kt == qt) {                                 // the diagonal tile: keys past the query
 #pragma unroll
                 for (int e = 0; e < 16; e++)
@@ -219,12 +225,10 @@ __device__ __forceinline__ void anvil_attn_fwd(const anvil_attn_io &a) {
             }
             mrun = mnew;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const vec vx = *(const vec *)&vs[(8 * (e >> 2) + 4 * h + (e & 3)) * P + DT * r];
+            for (int e = 0; e < 16; e++)
 #pragma unroll
                 for (int j = 0; j < DT; j++)
-                    oacc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(anvil_at_comp<D>(vx, j), st[e], oacc[j], 0, 0, 0);
-            }
+                    oacc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(anvil_at_comp<D>(vx[e], j), st[e], oacc[j], 0, 0, 0);
         }
     }
     __syncthreads();                                     // staged tiles read: LDS becomes partials
@@ -299,6 +303,7 @@ __device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
     }
     const long long srow = (long long)bh * (32 * NT) + query;
     const float mq = a.m[srow], rl = 1.f / a.l[srow];
+    if (live && s == 0 && h == 0) a.drow[srow] = drow;     // for the dK/dV launch, which follows
     anvil_f32x16 qacc[DT];
 #pragma unroll
     for (int j = 0; j < DT; j++)
@@ -328,6 +333,11 @@ __device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
                     dpt = __builtin_amdgcn_mfma_f32_32x32x2f32(vx[x], dr[c][x], dpt, 0, 0, 0);
                 }
             }
+            // the K operands of dS·K, read now: their LDS latency passes under P and dS
+            vec kc[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) kc[e] = *(const vec *)&ks[(8 * (e >> 2) + 4 * h + (e & 3)) * P + DT * r];
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const float pe = __builtin_amdgcn_exp2f(st[e] - mq) * rl;
@@ -339,12 +349,10 @@ __device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
                     if (8 * (e >> 2) + 4 * h + (e & 3) > r) st[e] = 0.f;
             }
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const vec kx = *(const vec *)&ks[(8 * (e >> 2) + 4 * h + (e & 3)) * P + DT * r];
+            for (int e = 0; e < 16; e++)
 #pragma unroll
                 for (int j = 0; j < DT; j++)
-                    qacc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(anvil_at_comp<D>(kx, j), st[e], qacc[j], 0, 0, 0);
-            }
+                    qacc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(anvil_at_comp<D>(kc[e], j), st[e], qacc[j], 0, 0, 0);
         }
     }
     __syncthreads();
@@ -366,6 +374,7 @@ __device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
     constexpr int DH = S::DH, DT = S::DT, P = S::P, C4 = D / 4;
     typedef typename anvil_vec_of<D>::type vec;
     __shared__ float lds[S::WORDS];
+    __shared__ float kvs[TI][2][S::TILE];                  // the workgroup's key tiles: K (scaled), V
     int bh, p;
     anvil_at_place(blockIdx.x, anvil_at_groups(NT, TI), a.BH, bh, p);
     const int n = bh / a.H, hh = bh - n * a.H;
@@ -374,66 +383,66 @@ __device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
     const int ti = w >> 2, s = w & 3;
     const int kt = ti ? NT - 1 - p : p;
     const bool live = !(ti && kt == p);
-    const int key = 32 * kt + r;
     const long long qoff = n * a.qn + hh * a.qh, ooff = n * a.on + hh * a.oh;
-    const float *qb = a.q + qoff, *db = a.dout + ooff, *ob = a.o + ooff;
-    const float *mb = a.m + (long long)bh * (32 * NT), *lb = a.l + (long long)bh * (32 * NT);
-    const float sc = a.alpha * 1.4426950408889634f;         // scores in base 2, as the forward's
-    anvil_f32x4 kr[DH / 4], vr[DH / 4];
+    const float *qb = a.q + qoff, *db = a.dout + ooff;
+    const long long sb = (long long)bh * (32 * NT);
+    const float *mb = a.m + sb, *lb = a.l + sb, *rb = a.drow + sb;
+    {
+        // the K and V rows of the workgroup's key tiles, K scaled by alpha · log2(e) (scores in base
+        // 2, as the forward's); visible after the first round's barrier
+        const float sc = a.alpha * 1.4426950408889634f;
+        constexpr int ITEMS = TI * 2 * 32 * C4, PK = (ITEMS + 256 * TI - 1) / (256 * TI);
+        anvil_f32x4 x[PK];
 #pragma unroll
-    for (int c = 0; c < DH / 4; c++) {
-        kr[c] = sc * *(const anvil_f32x4 *)(a.k + qoff + (long long)key * a.qs + DH * h + 4 * c);
-        vr[c] = *(const anvil_f32x4 *)(a.v + qoff + (long long)key * a.qs + DH * h + 4 * c);
+        for (int it = 0; it < PK; it++) {
+            const int i = threadIdx.x + 256 * TI * it;
+            const int c4 = i % C4, row = (i / C4) % 32, which = (i / (32 * C4)) & 1, t2 = i / (64 * C4);
+            const int kt2 = t2 ? NT - 1 - p : p;
+            if (i < ITEMS)
+                x[it] = *(const anvil_f32x4 *)((which ? a.v : a.k) + qoff + (long long)(32 * kt2 + row) * a.qs + 4 * c4);
+        }
+#pragma unroll
+        for (int it = 0; it < PK; it++) {
+            const int i = threadIdx.x + 256 * TI * it;
+            const int c4 = i % C4, row = (i / C4) % 32, which = (i / (32 * C4)) & 1, t2 = i / (64 * C4);
+            if (i < ITEMS) *(anvil_f32x4 *)&kvs[t2][which][row * P + 4 * c4] = which ? x[it] : sc * x[it];
+        }
     }
+    const float *kr = kvs[ti][0], *vr = kvs[ti][1];
     anvil_f32x16 kacc[DT], vacc[DT];
 #pragma unroll
     for (int j = 0; j < DT; j++)
 #pragma unroll
         for (int e = 0; e < 16; e++) kacc[j][e] = vacc[j][e] = 0.f;
     // staged query tile j of a round: Q at j·(2·TILE + 96), dO one TILE later, then m, 1 / l, Drow
-    constexpr int PER = 4 * 32 * C4 / (256 * TI), CH = PER > 1 ? 2 : 1;
+    constexpr int PER = 4 * 32 * C4 / (256 * TI);
     for (int rd = 0; p + 4 * rd < NT; rd++) {
         if (rd) __syncthreads();
-        // the round's loads in chunks of CH items, each chunk's loads issued before its LDS stores
+        // every load of the round, then the LDS stores (one wait for memory per round)
+        anvil_f32x4 qx[PER], dx[PER];
+        float sx[PER];
 #pragma unroll
-        for (int c0 = 0; c0 < PER; c0 += CH) {
-            anvil_f32x4 qx[CH], dx[CH], ox[CH];
-            float mx[CH], lx[CH];
-#pragma unroll
-            for (int ic = 0; ic < CH; ic++) {
-                const int i = threadIdx.x + 256 * TI * (c0 + ic);
-                const int c4 = i % C4, row = (i / C4) % 32, j = i / (32 * C4);
-                const int qt = p + 4 * rd + j;             // uniform over each group of C4 lanes
-                if (qt < NT) {
-                    const long long t = 32 * qt + row;
-                    qx[ic] = *(const anvil_f32x4 *)(qb + t * a.qs + 4 * c4);
-                    dx[ic] = *(const anvil_f32x4 *)(db + t * a.os + 4 * c4);
-                    ox[ic] = *(const anvil_f32x4 *)(ob + t * a.os + 4 * c4);
-                    if (c4 == 0) {
-                        mx[ic] = mb[t];
-                        lx[ic] = lb[t];
-                    }
-                }
+        for (int it = 0; it < PER; it++) {
+            const int i = threadIdx.x + 256 * TI * it;
+            const int c4 = i % C4, row = (i / C4) % 32, j = i / (32 * C4);
+            const int qt = p + 4 * rd + j;
+            if (qt < NT) {
+                const long long t = 32 * qt + row;
+                qx[it] = *(const anvil_f32x4 *)(qb + t * a.qs + 4 * c4);
+                dx[it] = *(const anvil_f32x4 *)(db + t * a.os + 4 * c4);
+                if (c4 < 3) sx[it] = (c4 == 0 ? mb : c4 == 1 ? lb : rb)[t];
             }
+        }
 #pragma unroll
-            for (int ic = 0; ic < CH; ic++) {
-                const int i = threadIdx.x + 256 * TI * (c0 + ic);
-                const int c4 = i % C4, row = (i / C4) % 32, j = i / (32 * C4);
-                const int qt = p + 4 * rd + j;
-                float *base = lds + j * (2 * S::TILE + 96);
-                float part = 0.f;
-                if (qt < NT) {
-                    *(anvil_f32x4 *)&base[row * P + 4 * c4] = qx[ic];
-                    *(anvil_f32x4 *)&base[S::TILE + row * P + 4 * c4] = dx[ic];
-                    part = dx[ic].x * ox[ic].x + dx[ic].y * ox[ic].y + dx[ic].z * ox[ic].z + dx[ic].w * ox[ic].w;
-                    if (c4 == 0) {
-                        base[2 * S::TILE + row] = mx[ic];
-                        base[2 * S::TILE + 32 + row] = 1.f / lx[ic];
-                    }
-                }
-#pragma unroll
-                for (int x = 1; x < C4; x <<= 1) part += __shfl_xor(part, x, 64);
-                if (qt < NT && c4 == 0) base[2 * S::TILE + 64 + row] = part;
+        for (int it = 0; it < PER; it++) {
+            const int i = threadIdx.x + 256 * TI * it;
+            const int c4 = i % C4, row = (i / C4) % 32, j = i / (32 * C4);
+            const int qt = p + 4 * rd + j;
+            float *base = lds + j * (2 * S::TILE + 96);
+            if (qt < NT) {
+                *(anvil_f32x4 *)&base[row * P + 4 * c4] = qx[it];
+                *(anvil_f32x4 *)&base[S::TILE + row * P + 4 * c4] = dx[it];
+                if (c4 < 3) base[2 * S::TILE + 32 * c4 + row] = c4 == 1 ? 1.f / sx[it] : sx[it];
             }
         }
         __syncthreads();
@@ -448,10 +457,12 @@ __device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
             for (int c = 0; c < DH / 4; c++) {
                 const anvil_f32x4 qx = *(const anvil_f32x4 *)&qs_[r * P + DH * h + 4 * c];
                 const anvil_f32x4 dx = *(const anvil_f32x4 *)&ds_[r * P + DH * h + 4 * c];
+                const anvil_f32x4 kx = *(const anvil_f32x4 *)&kr[r * P + DH * h + 4 * c];
+                const anvil_f32x4 vx = *(const anvil_f32x4 *)&vr[r * P + DH * h + 4 * c];
 #pragma unroll
                 for (int x = 0; x < 4; x++) {
-                    st = __builtin_amdgcn_mfma_f32_32x32x2f32(qx[x], kr[c][x], st, 0, 0, 0);
-                    dpt = __builtin_amdgcn_mfma_f32_32x32x2f32(dx[x], vr[c][x], dpt, 0, 0, 0);
+                    st = __builtin_amdgcn_mfma_f32_32x32x2f32(qx[x], kx[x], st, 0, 0, 0);
+                    dpt = __builtin_amdgcn_mfma_f32_32x32x2f32(dx[x], vx[x], dpt, 0, 0, 0);
                 }
             }
             // st[e], dpt[e]: S and dP at query row 8(e/4) + 4h + e%4 of tile qt, key r of tile kt
