@@ -418,6 +418,14 @@ def main() -> int:
         "roofline": roofline(prof, os.path.basename(lib.path)),
         "step_roofline": step_roofline(prof, ms / args.steps),
     }
+    # the box's measured stream-copy rate, labelled apart from the 8 TB/s published peak
+    cp = copy_run()
+    line["copy_ceiling"] = {"value": cp["value"], "unit": "GB/s", "frac_of_peak": round(cp["value"] / (PEAK_HBM / 1e9), 4),
+                            "kernel": f"plain copy, {cp['bytes_per_launch'] // 2 >> 20} MiB read + "
+                                      f"{cp['bytes_per_launch'] // 2 >> 20} MiB written per launch, "
+                                      f"mean of {cp['launches'] - 6} launches"}
+    if line["roofline"].get("unit") == "GB/s":
+        line["roofline"]["frac_of_copy"] = round(line["roofline"]["achieved"] / cp["value"], 4)
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_steps)
         line["cpu_baseline"] = cpu
