@@ -47,12 +47,12 @@ struct anvil_attn_io {
 
 // LDS row pitch of a staged 32 x D tile: D + 4 floats keeps the row-form reads (32 rows, one
 // 16-byte column each) on distinct banks
-template <int D, int TI> struct anvil_at_shape {
+template <int D, int TI, int SL = 4> struct anvil_at_shape {
     static constexpr int P = D + 4;
     static constexpr int DH = D / 2, DT = D / 32;
     static constexpr int TILE = 32 * P;
     // forward and dQ: K and V tiles; dK/dV: Q and dO tiles plus m, l, Drow
-    static constexpr int STAGE = 4 * (2 * TILE + 96);
+    static constexpr int STAGE = SL * (2 * TILE + 96);
     // partial output tiles of the 4·TI wavefronts, one accumulator register (64 lanes) per LDS row of
     // 65 words: written lane by lane, and read one output row at a time (64 features on 64 lanes,
     // drawn from two lanes' registers e = 0..15 of DT tiles) without two lanes meeting on a bank
@@ -76,6 +76,10 @@ __device__ __forceinline__ void anvil_at_place(int L, int per, int BH, int &bh, 
 
 // workgroups per head: one per tile, or one per pair of tiles p, NT − 1 − p
 __host__ __device__ constexpr int anvil_at_groups(int NT, int TI) { return TI == 2 ? (NT + 1) / 2 : NT; }
+
+// tiles of the other side staged at once by the forward and dQ: all of them when a pair's 8 fit
+// in LDS (T ≤ 256: one round, no barrier between a wavefront's tiles), else rounds of 4
+__host__ __device__ constexpr int anvil_at_slots(int NT, int TI) { return TI == 2 && NT > 4 && NT <= 8 ? 8 : 4; }
 
 template <int D>
 __device__ __forceinline__ float anvil_at_comp(const typename anvil_vec_of<D>::type &x, int j) {
@@ -113,30 +117,30 @@ __device__ __forceinline__ void anvil_at_store(const float *part, int ti, int s,
 // The K and V tiles 4·rd .. 4·rd + 3 (those ≤ last) of one head, in two steps: the lane's share of
 // them loaded into registers (all loads issued together), then stored to LDS. The loads of round
 // rd + 1 are issued before round rd's products, so they are in flight while those run.
-template <int D, int TI> struct anvil_at_kv { anvil_f32x4 x[4 * 2 * 32 * (D / 4) / (256 * TI)]; };
+template <int D, int TI, int SL> struct anvil_at_kv { anvil_f32x4 x[SL * 2 * 32 * (D / 4) / (256 * TI)]; };
 
-template <int D, int TI>
-__device__ __forceinline__ void anvil_at_load_kv(anvil_at_kv<D, TI> &b, const float *kb, const float *vb, long long qs,
-                                                 int rd, int last) {
-    constexpr int C4 = D / 4, PER = 4 * 2 * 32 * C4 / (256 * TI);
+template <int D, int TI, int SL>
+__device__ __forceinline__ void anvil_at_load_kv(anvil_at_kv<D, TI, SL> &b, const float *kb, const float *vb,
+                                                 long long qs, int rd, int last) {
+    constexpr int C4 = D / 4, PER = SL * 2 * 32 * C4 / (256 * TI);
 #pragma unroll
     for (int it = 0; it < PER; it++) {
         const int i = threadIdx.x + 256 * TI * it;
         const int c4 = i % C4, row = (i / C4) % 32, which = (i / (32 * C4)) & 1, j = i / (64 * C4);
-        const int kt = 4 * rd + j;
+        const int kt = SL * rd + j;
         if (kt <= last) b.x[it] = *(const anvil_f32x4 *)((which ? vb : kb) + (long long)(32 * kt + row) * qs + 4 * c4);
     }
 }
 
-template <int D, int TI>
-__device__ __forceinline__ void anvil_at_put_kv(float *lds, const anvil_at_kv<D, TI> &b, int rd, int last) {
-    typedef anvil_at_shape<D, TI> S;
-    constexpr int C4 = D / 4, PER = 4 * 2 * 32 * C4 / (256 * TI);
+template <int D, int TI, int SL>
+__device__ __forceinline__ void anvil_at_put_kv(float *lds, const anvil_at_kv<D, TI, SL> &b, int rd, int last) {
+    typedef anvil_at_shape<D, TI, SL> S;
+    constexpr int C4 = D / 4, PER = SL * 2 * 32 * C4 / (256 * TI);
 #pragma unroll
     for (int it = 0; it < PER; it++) {
         const int i = threadIdx.x + 256 * TI * it;
         const int c4 = i % C4, row = (i / C4) % 32, which = (i / (32 * C4)) & 1, j = i / (64 * C4);
-        if (4 * rd + j <= last) *(anvil_f32x4 *)&lds[(2 * j + which) * S::TILE + row * S::P + 4 * c4] = b.x[it];
+        if (SL * rd + j <= last) *(anvil_f32x4 *)&lds[(2 * j + which) * S::TILE + row * S::P + 4 * c4] = b.x[it];
     }
 }
 
@@ -144,7 +148,8 @@ __device__ __forceinline__ void anvil_at_put_kv(float *lds, const anvil_at_kv<D,
 // grid: anvil_at_groups<NT, TI> · BH workgroups of 256·TI lanes
 template <int D, int NT, int TI>
 __device__ __forceinline__ void anvil_attn_fwd(const anvil_attn_io &a) {
-    typedef anvil_at_shape<D, TI> S;
+    constexpr int SL = anvil_at_slots(NT, TI);
+    typedef anvil_at_shape<D, TI, SL> S;
     constexpr int DH = S::DH, DT = S::DT, P = S::P;
     typedef typename anvil_vec_of<D>::type vec;
     __shared__ float lds[S::WORDS];
@@ -172,16 +177,19 @@ __device__ __forceinline__ void anvil_attn_fwd(const anvil_attn_io &a) {
         for (int e = 0; e < 16; e++) oacc[j][e] = 0.f;
     float mrun = -__builtin_inff(), lrun = 0.f;
     const int last = TI == 2 ? NT - 1 - p : p;           // the last key tile the workgroup needs
-    anvil_at_kv<D, TI> buf;
-    anvil_at_load_kv<D, TI>(buf, kb, vb, a.qs, 0, last);
-    for (int rd = 0; rd <= last / 4; rd++) {
+    anvil_at_kv<D, TI, SL> buf;
+    anvil_at_load_kv<D, TI, SL>(buf, kb, vb, a.qs, 0, last);
+    for (int rd = 0; rd <= last / SL; rd++) {
         if (rd) __syncthreads();
-        anvil_at_put_kv<D, TI>(lds, buf, rd, last);
+        anvil_at_put_kv<D, TI, SL>(lds, buf, rd, last);
         __syncthreads();
-        if (rd + 1 <= last / 4) anvil_at_load_kv<D, TI>(buf, kb, vb, a.qs, rd + 1, last);
-        const int kt = 4 * rd + s;
-        if (live && kt <= qt) {
-            const float *ks = lds + (2 * s) * S::TILE, *vs = lds + (2 * s + 1) * S::TILE;
+        if (rd + 1 <= last / SL) anvil_at_load_kv<D, TI, SL>(buf, kb, vb, a.qs, rd + 1, last);
+        // the wavefront's staged tiles of the round, back to back: slots s, s + 4, ...
+#pragma unroll
+        for (int u = 0; u < SL / 4; u++) {
+            const int slot = s + 4 * u, kt = SL * rd + slot;
+            if (!live || kt > qt) continue;
+            const float *ks = lds + (2 * slot) * S::TILE, *vs = lds + (2 * slot + 1) * S::TILE;
             anvil_f32x16 st;
 #pragma unroll
             for (int e = 0; e < 16; e++) st[e] = 0.f;
@@ -270,7 +278,8 @@ __device__ __forceinline__ void anvil_attn_fwd(const anvil_attn_io &a) {
 // grid: anvil_at_groups<NT, TI> · BH workgroups of 256·TI lanes
 template <int D, int NT, int TI, bool ACC>
 __device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
-    typedef anvil_at_shape<D, TI> S;
+    constexpr int SL = anvil_at_slots(NT, TI);
+    typedef anvil_at_shape<D, TI, SL> S;
     constexpr int DH = S::DH, DT = S::DT, P = S::P;
     typedef typename anvil_vec_of<D>::type vec;
     __shared__ float lds[S::WORDS];
@@ -310,16 +319,31 @@ __device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
 #pragma unroll
         for (int e = 0; e < 16; e++) qacc[j][e] = 0.f;
     const int last = TI == 2 ? NT - 1 - p : p;
-    anvil_at_kv<D, TI> buf;
-    anvil_at_load_kv<D, TI>(buf, kb, vb, a.qs, 0, last);
-    for (int rd = 0; rd <= last / 4; rd++) {
+    // eight tiles (one round) are staged in two halves of four: the registers of the whole round
+    // would not fit beside the query's Q and dO rows
+    constexpr bool halves = SL == 8;
+    anvil_at_kv<D, TI, halves ? 4 : SL> buf;
+    if constexpr (!halves) anvil_at_load_kv<D, TI, SL>(buf, kb, vb, a.qs, 0, last);
+    for (int rd = 0; rd <= last / SL; rd++) {
         if (rd) __syncthreads();
-        anvil_at_put_kv<D, TI>(lds, buf, rd, last);
+        if constexpr (halves) {
+            anvil_at_load_kv<D, TI, 4>(buf, kb, vb, a.qs, 0, last);
+            anvil_at_put_kv<D, TI, 4>(lds, buf, 0, last);
+            anvil_at_load_kv<D, TI, 4>(buf, kb, vb, a.qs, 1, last);
+            anvil_at_put_kv<D, TI, 4>(lds + 8 * S::TILE, buf, 1, last);
+        } else {
+            anvil_at_put_kv<D, TI, SL>(lds, buf, rd, last);
+        }
         __syncthreads();
-        if (rd + 1 <= last / 4) anvil_at_load_kv<D, TI>(buf, kb, vb, a.qs, rd + 1, last);
-        const int kt = 4 * rd + s;
-        if (live && kt <= qt) {
-            const float *ks = lds + (2 * s) * S::TILE, *vs = lds + (2 * s + 1) * S::TILE;
+        if constexpr (!halves) {
+            if (rd + 1 <= last / SL) anvil_at_load_kv<D, TI, SL>(buf, kb, vb, a.qs, rd + 1, last);
+        }
+        // the wavefront's staged tiles of the round, back to back: slots s, s + 4, ...
+#pragma unroll
+        for (int u = 0; u < SL / 4; u++) {
+            const int slot = s + 4 * u, kt = SL * rd + slot;
+            if (!live || kt > qt) continue;
+            const float *ks = lds + (2 * slot) * S::TILE, *vs = lds + (2 * slot + 1) * S::TILE;
             anvil_f32x16 st, dpt;
 #pragma unroll
             for (int e = 0; e < 16; e++) st[e] = dpt[e] = 0.f;
