@@ -669,4 +669,9 @@ PROGRAMS = [
     # end in a partial group of 4
     {"name": "c5_conv12", "source": C5, "consts": {"STEPS": 2, "NB": 32, "C1": 12, "C2": 16, "HID": 32},
      "interp": True, "keep": ["net.c1.W", "net.c1.b", "net.c2.W", "net.fc1.W"]},
+    # C4 with five 32-row tiles per head: the training attention's workgroups take the tile pairs
+    # (0, 4), (1, 3) and the middle tile 2 alone, with all of a pair's key tiles staged at once
+    {"name": "c4_t160", "source": C4,
+     "consts": {"STEPS": 2, "BATCH": 2, "T": 160, "D": 128, "HEADS": 2, "LAYERS": 1}, "interp": True,
+     "keep": ["net.tok", "net.layers.0.Wqkv", "net.layers.0.Wout", "net.head.W"]},
 ]

@@ -8,14 +8,15 @@ exp to be exactly 0 in float32, or whose probabilities another statement reads, 
 The arena keeps the row maxima and the attention output (which the fused backward reads and the
 IR's backward does not) alive up to the backward. The GPU results of the fused launches are held to
 the reference's own vectors by the C4 programs of tests/test_hip_gpu.py (c4_mid, c4_full2,
-c4_t256_2).
+c4_t160: pairs of tiles with an odd middle one, c4_t256_2).
 """
 import pytest
 
 from fixtures import load_ir
 
-LAYERS = {"c4_full2": 4, "c4_t256_2": 4, "c4_mid": 1, "c4_small": 0}
-SHAPES = {"c4_full2": (16, 4, 64, 64), "c4_t256_2": (16, 4, 256, 64), "c4_mid": (4, 2, 32, 32)}
+LAYERS = {"c4_full2": 4, "c4_t256_2": 4, "c4_mid": 1, "c4_small": 0, "c4_t160": 1}
+SHAPES = {"c4_full2": (16, 4, 64, 64), "c4_t256_2": (16, 4, 256, 64), "c4_mid": (4, 2, 32, 32),
+          "c4_t160": (2, 2, 160, 64)}
 
 
 def _gen(prog, data):
