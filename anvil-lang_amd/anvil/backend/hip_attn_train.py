@@ -529,6 +529,10 @@ class _AttnTrainPlan(Plan):
         self.TI = int(os.environ.get("ANVIL_ATTN_TI", "0")) or (1 if self.NT <= 2 else 2)
         self.threads = 256 * self.TI
         self.groups = self.NT if self.TI == 1 else (self.NT + 1) // 2
+        # the backward as one launch whose workgroups alternate between dQ and dK/dV (each
+        # computing Drow) up to five tiles per head, where the two launches are mostly fixed cost;
+        # two launches (dQ writing Drow for dK/dV) above
+        self.combined = self.NT <= 5
 
     def grid(self):
         return self.groups * self.sh.B * self.sh.H, self.threads
@@ -545,7 +549,8 @@ class _AttnTrainPlan(Plan):
                  f"    a.m = {m}; a.l = {l};",
                  f"    a.H = {sh.H}; a.BH = {sh.B * sh.H}; a.alpha = {flit(sh.alpha)};"]
         if backward:
-            g, do, dr = self.use_buf(sh.G), self.use_buf(sh.dO), self.use_buf(sh.DL)
+            g, do = self.use_buf(sh.G), self.use_buf(sh.dO)
+            dr = "nullptr" if self.combined else self.use_buf(sh.DL)
             lines += [f"    a.dout = {do} + {sh.o0}LL; a.drow = {dr};",
                       f"    a.dq = {g} + {sh.q0}LL; a.dk = {g} + {sh.k0}LL; a.dv = {g} + {sh.v0}LL;"]
         else:
@@ -586,15 +591,25 @@ class AttnTrainFwdPlan(_AttnTrainPlan):
 
 
 class AttnTrainBwdPlan(_AttnTrainPlan):
-    """The dQ launch; second() is the dK/dV launch, which follows it."""
+    """The backward: one launch of both kinds of workgroup, or the dQ launch with second() the
+    dK/dV launch that follows it."""
     kind = "attention-train-dq"
-    two_launches = True
+
+    def __init__(self, gen, kernels, name, sh):
+        super().__init__(gen, kernels, name, sh)
+        self.two_launches = not self.combined
+        if self.combined:
+            self.kind = "attention-train-bwd"
+
+    def grid(self):
+        blocks, threads = super().grid()
+        return (2 * blocks if self.combined else blocks), threads
 
     def writes(self) -> set:
-        return {self.sh.G, self.sh.DL}
+        return {self.sh.G} if self.combined else {self.sh.G, self.sh.DL}
 
     def full_writes(self) -> set:
-        return {self.sh.G.id, self.sh.DL.id}
+        return {b.id for b in self.writes()}
 
     def extra_reads(self) -> set:
         """What the launches read beyond the IR kernels they replace: the forward's row maxima and
@@ -603,6 +618,8 @@ class AttnTrainBwdPlan(_AttnTrainPlan):
 
     def cost(self):
         sh = self.sh
+        if self.combined:                  # both kinds of workgroup: dQ's 3 products, dK/dV's 4
+            return self.units() * 7 * 2 * 32 * 32 * sh.D, self.tensor_bytes(13) + 4 * 4 * sh.B * sh.H * sh.T
         return self.units() * 3 * 2 * 32 * 32 * sh.D, self.tensor_bytes(6) + 4 * 2 * sh.B * sh.H * sh.T
 
     def second(self):
@@ -611,6 +628,12 @@ class AttnTrainBwdPlan(_AttnTrainPlan):
     def source(self) -> str:
         sh = self.sh
         io = self.io(True)
+        if self.combined:
+            return "\n".join(
+                [f"// attention-train backward: {' + '.join(k.name for k in self.kernels)} · {sh.B * sh.H} heads of "
+                 f"{sh.T} x {sh.T}, D = {sh.D}, causal · dQ and dK/dV workgroups side by side, P and dS never stored",
+                 self.header(self.threads)] + io +
+                [f"    anvil_attn_bwd<{sh.D}, {self.NT}, {self.TI}, false>(a);", "}"])
         return "\n".join(
             [f"// attention-train dQ: {' + '.join(k.name for k in self.kernels)} · {sh.B * sh.H} heads of "
              f"{sh.T} x {sh.T}, D = {sh.D}, causal · P recomputed from Q, K, m, l; dS stays in registers",

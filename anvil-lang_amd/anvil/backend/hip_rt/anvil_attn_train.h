@@ -277,14 +277,11 @@ __device__ __forceinline__ void anvil_attn_fwd(const anvil_attn_io &a) {
 // dQ for the query tiles p and NT − 1 − p of head bh
 // grid: anvil_at_groups<NT, TI> · BH workgroups of 256·TI lanes
 template <int D, int NT, int TI, bool ACC>
-__device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
+__device__ __forceinline__ void anvil_attn_bwd_q_body(const anvil_attn_io &a, float *lds, int bh, int p) {
     constexpr int SL = anvil_at_slots(NT, TI);
     typedef anvil_at_shape<D, TI, SL> S;
     constexpr int DH = S::DH, DT = S::DT, P = S::P;
     typedef typename anvil_vec_of<D>::type vec;
-    __shared__ float lds[S::WORDS];
-    int bh, p;
-    anvil_at_place(blockIdx.x, anvil_at_groups(NT, TI), a.BH, bh, p);
     const int n = bh / a.H, hh = bh - n * a.H;
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -312,7 +309,7 @@ __device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
     }
     const long long srow = (long long)bh * (32 * NT) + query;
     const float mq = a.m[srow], rl = 1.f / a.l[srow];
-    if (live && s == 0 && h == 0) a.drow[srow] = drow;     // for the dK/dV launch, which follows
+    if (a.drow && live && s == 0 && h == 0) a.drow[srow] = drow;    // for a dK/dV launch that follows
     anvil_f32x16 qacc[DT];
 #pragma unroll
     for (int j = 0; j < DT; j++)
@@ -392,15 +389,13 @@ __device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
 
 // dK and dV for the key tiles p and NT − 1 − p of head bh
 // grid: anvil_at_groups<NT, TI> · BH workgroups of 256·TI lanes
-template <int D, int NT, int TI, bool ACC>
-__device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
+// OWN: Drow computed here from dO and O while staging (when no dQ launch precedes this one)
+template <int D, int NT, int TI, bool ACC, bool OWN>
+__device__ __forceinline__ void anvil_attn_bwd_kv_body(const anvil_attn_io &a, float *lds, int bh, int p) {
     typedef anvil_at_shape<D, TI> S;
     constexpr int DH = S::DH, DT = S::DT, P = S::P, C4 = D / 4;
     typedef typename anvil_vec_of<D>::type vec;
-    __shared__ float lds[S::WORDS];
-    __shared__ float kvs[TI][2][S::TILE];                  // the workgroup's key tiles: K (scaled), V
-    int bh, p;
-    anvil_at_place(blockIdx.x, anvil_at_groups(NT, TI), a.BH, bh, p);
+    float (*kvs)[2][S::TILE] = (float (*)[2][S::TILE])(lds + S::WORDS);     // the workgroup's key tiles: K (scaled), V
     const int n = bh / a.H, hh = bh - n * a.H;
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -408,9 +403,9 @@ __device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
     const int kt = ti ? NT - 1 - p : p;
     const bool live = !(ti && kt == p);
     const long long qoff = n * a.qn + hh * a.qh, ooff = n * a.on + hh * a.oh;
-    const float *qb = a.q + qoff, *db = a.dout + ooff;
+    const float *qb = a.q + qoff, *db = a.dout + ooff, *ob = a.o + ooff;
     const long long sb = (long long)bh * (32 * NT);
-    const float *mb = a.m + sb, *lb = a.l + sb, *rb = a.drow + sb;
+    const float *mb = a.m + sb, *lb = a.l + sb, *rb = OWN ? nullptr : a.drow + sb;
     {
         // the K and V rows of the workgroup's key tiles, K scaled by alpha · log2(e) (scores in base
         // 2, as the forward's); visible after the first round's barrier
@@ -443,7 +438,7 @@ __device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
     for (int rd = 0; p + 4 * rd < NT; rd++) {
         if (rd) __syncthreads();
         // every load of the round, then the LDS stores (one wait for memory per round)
-        anvil_f32x4 qx[PER], dx[PER];
+        anvil_f32x4 qx[PER], dx[PER], ox[OWN ? PER : 1];
         float sx[PER];
 #pragma unroll
         for (int it = 0; it < PER; it++) {
@@ -454,7 +449,8 @@ __device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
                 const long long t = 32 * qt + row;
                 qx[it] = *(const anvil_f32x4 *)(qb + t * a.qs + 4 * c4);
                 dx[it] = *(const anvil_f32x4 *)(db + t * a.os + 4 * c4);
-                if (c4 < 3) sx[it] = (c4 == 0 ? mb : c4 == 1 ? lb : rb)[t];
+                if constexpr (OWN) ox[it] = *(const anvil_f32x4 *)(ob + t * a.os + 4 * c4);
+                if (c4 < (OWN ? 2 : 3)) sx[it] = (c4 == 0 ? mb : c4 == 1 ? lb : rb)[t];
             }
         }
 #pragma unroll
@@ -466,7 +462,15 @@ __device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
             if (qt < NT) {
                 *(anvil_f32x4 *)&base[row * P + 4 * c4] = qx[it];
                 *(anvil_f32x4 *)&base[S::TILE + row * P + 4 * c4] = dx[it];
-                if (c4 < 3) base[2 * S::TILE + 32 * c4 + row] = c4 == 1 ? 1.f / sx[it] : sx[it];
+                if (c4 < (OWN ? 2 : 3)) base[2 * S::TILE + 32 * c4 + row] = c4 == 1 ? 1.f / sx[it] : sx[it];
+            }
+            if constexpr (OWN) {
+                // Drow of the row: its C4 lanes' partial dot products, added across them
+                float part = qt < NT ? dx[it].x * ox[it].x + dx[it].y * ox[it].y + dx[it].z * ox[it].z +
+                                           dx[it].w * ox[it].w : 0.f;
+#pragma unroll
+                for (int x = 1; x < C4; x <<= 1) part += __shfl_xor(part, x, 64);
+                if (qt < NT && c4 == 0) base[2 * S::TILE + 64 + row] = part;
             }
         }
         __syncthreads();
@@ -532,6 +536,40 @@ __device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
     if (live)
         anvil_at_store<D, ACC>(lds, ti, s, lane, a.dk + qoff + (long long)(32 * kt) * a.qs, a.qs, nullptr, nullptr,
                                a.alpha);
+}
+
+// The backward as two launches: dQ (writes Drow), then dK/dV.
+// grid: anvil_at_groups<NT, TI> · BH workgroups of 256·TI lanes each
+template <int D, int NT, int TI, bool ACC>
+__device__ __forceinline__ void anvil_attn_bwd_q(const anvil_attn_io &a) {
+    __shared__ float lds[anvil_at_shape<D, TI, anvil_at_slots(NT, TI)>::WORDS];
+    int bh, p;
+    anvil_at_place(blockIdx.x, anvil_at_groups(NT, TI), a.BH, bh, p);
+    anvil_attn_bwd_q_body<D, NT, TI, ACC>(a, lds, bh, p);
+}
+
+template <int D, int NT, int TI, bool ACC>
+__device__ __forceinline__ void anvil_attn_bwd_kv(const anvil_attn_io &a) {
+    typedef anvil_at_shape<D, TI> S;
+    __shared__ float lds[S::WORDS + TI * 2 * S::TILE];
+    int bh, p;
+    anvil_at_place(blockIdx.x, anvil_at_groups(NT, TI), a.BH, bh, p);
+    anvil_attn_bwd_kv_body<D, NT, TI, ACC, false>(a, lds, bh, p);
+}
+
+// The backward as one launch whose workgroups alternate between the two (dK/dV computing Drow
+// itself): for short heads, where the launches are mostly fixed cost and running the two side by
+// side halves it. grid: 2 · anvil_at_groups<NT, TI> · BH workgroups of 256·TI lanes.
+template <int D, int NT, int TI, bool ACC>
+__device__ __forceinline__ void anvil_attn_bwd(const anvil_attn_io &a) {
+    typedef anvil_at_shape<D, TI, anvil_at_slots(NT, TI)> SQ;
+    typedef anvil_at_shape<D, TI> SK;
+    constexpr int WQ = SQ::WORDS, WK = SK::WORDS + TI * 2 * SK::TILE;
+    __shared__ float lds[WQ > WK ? WQ : WK];
+    int bh, x;
+    anvil_at_place(blockIdx.x, 2 * anvil_at_groups(NT, TI), a.BH, bh, x);
+    if (x & 1) anvil_attn_bwd_kv_body<D, NT, TI, ACC, true>(a, lds, bh, x >> 1);
+    else anvil_attn_bwd_q_body<D, NT, TI, ACC>(a, lds, bh, x >> 1);
 }
 
 #endif

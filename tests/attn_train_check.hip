@@ -20,14 +20,25 @@ static hipError_t last_error = hipSuccess;
 extern "C" const char *attn_train_check_error(void) { return hipGetErrorString(last_error); }
 
 template <int D, int NT, int TI>
-static int run(const anvil_attn_io &a, int BH) {
+__global__ void __launch_bounds__(256 * TI) at_bwd(anvil_attn_io a) { anvil_attn_bwd<D, NT, TI, false>(a); }
+
+// the backward as two launches (dQ writing Drow, then dK/dV) or, combined, as one launch of both
+// kinds of workgroup
+template <int D, int NT, int TI>
+static int run(anvil_attn_io a, int BH, int combined) {
     const dim3 grid(anvil_at_groups(NT, TI) * BH), block(256 * TI);
     hipLaunchKernelGGL((at_fwd<D, NT, TI>), grid, block, 0, 0, a);
     if ((last_error = hipGetLastError()) != hipSuccess) return -3;
-    hipLaunchKernelGGL((at_dq<D, NT, TI>), grid, block, 0, 0, a);
-    if ((last_error = hipGetLastError()) != hipSuccess) return -4;
-    hipLaunchKernelGGL((at_dkv<D, NT, TI>), grid, block, 0, 0, a);
-    if ((last_error = hipGetLastError()) != hipSuccess) return -5;
+    if (combined) {
+        a.drow = nullptr;
+        hipLaunchKernelGGL((at_bwd<D, NT, TI>), dim3(2 * grid.x), block, 0, 0, a);
+        if ((last_error = hipGetLastError()) != hipSuccess) return -4;
+    } else {
+        hipLaunchKernelGGL((at_dq<D, NT, TI>), grid, block, 0, 0, a);
+        if ((last_error = hipGetLastError()) != hipSuccess) return -4;
+        hipLaunchKernelGGL((at_dkv<D, NT, TI>), grid, block, 0, 0, a);
+        if ((last_error = hipGetLastError()) != hipSuccess) return -5;
+    }
     return (last_error = hipDeviceSynchronize()) == hipSuccess ? 0 : -2;
 }
 
@@ -42,9 +53,10 @@ extern "C" int attn_train_check_shapes(int *out, int cap) {
     return n / 3;
 }
 
-// Forward, then dQ (which writes Drow), then dK/dV: O, m (base 2), l, Drow and dQKV written.
-extern "C" int attn_train_check(int D, int NT, int TI, int B, int H, float alpha, const float *qkv, float *o,
-                                float *m, float *l, const float *dout, float *drow, float *dqkv) {
+// The forward, then the backward (combined or not): O, m (base 2), l, dQKV (and Drow when not
+// combined) written.
+extern "C" int attn_train_check(int D, int NT, int TI, int combined, int B, int H, float alpha, const float *qkv,
+                                float *o, float *m, float *l, const float *dout, float *drow, float *dqkv) {
     const int T = 32 * NT, HD = H * D;
     anvil_attn_io a;
     a.q = qkv; a.k = qkv + HD; a.v = qkv + 2 * HD;
@@ -53,7 +65,7 @@ extern "C" int attn_train_check(int D, int NT, int TI, int B, int H, float alpha
     a.m = m; a.l = l; a.drow = drow;
     a.dq = dqkv; a.dk = dqkv + HD; a.dv = dqkv + 2 * HD;
     a.H = H; a.BH = B * H; a.alpha = alpha;
-#define ANVIL_AT_RUN(d, nt, ti) if (D == d && NT == nt && TI == ti) return run<d, nt, ti>(a, B * H);
+#define ANVIL_AT_RUN(d, nt, ti) if (D == d && NT == nt && TI == ti) return run<d, nt, ti>(a, B * H, combined);
     ANVIL_AT_SHAPES(ANVIL_AT_RUN)
 #undef ANVIL_AT_RUN
     return -1;

@@ -5,7 +5,8 @@ tests/attn_train_check.hip (built by __graft_entry__.build()) launches the forwa
 kernels on device buffers in the generated code's layout. Here the results are compared with a
 float64 NumPy evaluation of the definitions: S = alpha·Q Kᵀ with keys past the query masked, P its
 row softmax, O = P V; dP = dO Vᵀ, dS = P ⊙ (dP − rowsum(dP ⊙ P)), dQ = alpha·dS K, dK = alpha·dSᵀ Q,
-dV = Pᵀ dO. The shapes cover one tile per workgroup (T = 64), pairs of tiles with an odd middle one
+dV = Pᵀ dO, with the backward as two launches and as one. The shapes cover one tile per workgroup (T = 64),
+pairs of tiles with an odd middle one
 (T = 96, 160), staging in rounds of four and in one round of eight, heads of 32 and 64, and a batch ×
 heads count that is not a multiple of 8 (the workgroups then go to the XCDs in plain order). The C4
 programs of tests/test_hip_gpu.py hold the same kernels to the reference interpreter's vectors.
@@ -28,7 +29,7 @@ def _lib():
         pytest.fail(f"{LIB} is missing: run __graft_entry__.build() first")
     lib = ctypes.CDLL(LIB)
     lib.attn_train_check.restype = ctypes.c_int
-    lib.attn_train_check.argtypes = [ctypes.c_int] * 5 + [ctypes.c_float] + [ctypes.c_void_p] * 7
+    lib.attn_train_check.argtypes = [ctypes.c_int] * 6 + [ctypes.c_float] + [ctypes.c_void_p] * 7
     lib.attn_train_check_error.restype = ctypes.c_char_p
     return lib
 
@@ -61,8 +62,9 @@ def test_the_library_instantiates_the_plan_choices():
     assert shapes and all(d in (32, 64) and (ti == 1) == (nt <= 2) for d, nt, ti in shapes)
 
 
+@pytest.mark.parametrize("combined", [0, 1])
 @pytest.mark.parametrize("B,H", [(2, 3)])
-def test_kernels_match_float64(B, H):
+def test_kernels_match_float64(B, H, combined):
     from anvil.hip_function import DeviceArray          # the HIP runtime the libraries link
     lib = _lib()
     rng = np.random.default_rng(5)
@@ -76,8 +78,8 @@ def test_kernels_match_float64(B, H):
         out = {"o": nan((B, T, H, D)), "m": nan((B, H, T)), "l": nan((B, H, T)), "drow": nan((B, H, T)),
                "dqkv": nan((B, T, 3, H, D))}
         try:
-            print(f"attention kernels D={D} T={T} TI={TI} B={B} H={H}", flush=True)
-            rc = lib.attn_train_check(D, NT, TI, B, H, alpha, ins["qkv"].data_ptr(), out["o"].data_ptr(),
+            print(f"attention kernels D={D} T={T} TI={TI} B={B} H={H} backward in one launch: {combined}", flush=True)
+            rc = lib.attn_train_check(D, NT, TI, combined, B, H, alpha, ins["qkv"].data_ptr(), out["o"].data_ptr(),
                                       out["m"].data_ptr(), out["l"].data_ptr(), ins["do"].data_ptr(),
                                       out["drow"].data_ptr(), out["dqkv"].data_ptr())
             assert rc == 0, (D, NT, TI, rc, lib.attn_train_check_error().decode())
@@ -89,7 +91,7 @@ def test_kernels_match_float64(B, H):
             for h in range(H):
                 q, k, v = (qkv[n, :, i, h].astype(np.float64) for i in range(3))
                 o, m, l, dq, dk, dv = _reference(q, k, v, do[n, :, h].astype(np.float64), alpha)
-                where = f"D={D} T={T} TI={TI} n={n} h={h}"
+                where = f"D={D} T={T} TI={TI} combined={combined} n={n} h={h}"
                 np.testing.assert_allclose(got["o"][n, :, h], o, rtol=0, atol=2e-6 * np.abs(o).max(), err_msg=where)
                 # m is the row maximum in base 2 (scores scaled by log2 e)
                 np.testing.assert_allclose(got["m"][n, h] / LOG2E, m, rtol=2e-6, atol=2e-6, err_msg=where)
