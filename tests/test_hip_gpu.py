@@ -269,9 +269,10 @@ def test_gpu_checkpoint_save_then_load(tmp_path):
     assert out1.split("sum")[1] == out2.split("sum")[1]
 
 
-@pytest.mark.parametrize("name", ["c2_small", "logreg", "c4_small"])
+@pytest.mark.parametrize("name", ["c2_small", "logreg", "c4_small", "c4_mid", "c4_t160"])
 def test_gpu_graph_replay_matches_reference(name):
-    """The same programs with loop bodies captured once as HIP graphs and replayed."""
+    """The same programs with loop bodies captured once as HIP graphs and replayed (c4_mid and
+    c4_t160: with the training attention's launches among the captured ones)."""
     print(f"gpu graphs {name}", flush=True)
     keep = kept_buffers(name)
     rc, out, err, arrays = run_program(name, emulate=False, keep=keep, timeout=300, env_extra={"ANVIL_HIP_GRAPHS": "1"})
