@@ -1274,7 +1274,7 @@ class HipLibrary:
         self.source = source
         self.lib = ctypes.CDLL(path)
         for fn in ("anvil_main", "anvil_entry", "anvil_entry_device", "anvil_init", "anvil_sync_device",
-                   "anvil_profile_count", "anvil_marks_count"):
+                   "anvil_profile_count", "anvil_marks_count", "anvil_marks_window"):
             getattr(self.lib, fn).restype = ctypes.c_int
         self.lib.anvil_profile_ms.restype = ctypes.c_double
         self.lib.anvil_profile_ms.argtypes = [ctypes.c_int]
@@ -1288,6 +1288,7 @@ class HipLibrary:
         self.lib.anvil_profile_label.argtypes = [ctypes.c_int]
         self.lib.anvil_profile_enable.argtypes = [ctypes.c_int]
         self.lib.anvil_marks_select.argtypes = [ctypes.c_char_p]
+        self.lib.anvil_marks_window.argtypes = [ctypes.c_int, ctypes.c_int]
         self.lib.anvil_marks_elapsed_ms.restype = ctypes.c_double
         self.lib.anvil_marks_elapsed_ms.argtypes = [ctypes.c_int, ctypes.c_int]
         self.lib.anvil_arena_bytes.restype = ctypes.c_longlong

@@ -7,9 +7,10 @@ U{0..9}, Linear-default init after seed(1)) as the reference front end produces 
 (tests/golden/ir/c2_wide_mlp.json). The program generates its own synthetic data on the device.
 
 A step is one training iteration: the batch gather, forward, backward and Adam update. The library
-records a device event at the start of every iteration of the batch loop; the timed region is the K
-iterations after W warm-up ones, all on the library's stream, with the device synchronized before
-and after. `value` is samples/s over those K steps.
+records a device event at the start of iterations W and W + K of the batch loop (it counts the
+others and records nothing for them); the timed region is the K iterations between, all on the
+library's stream, with the device synchronized before and after. `value` is samples/s over those K
+steps.
 
 The roofline object is for the generated kernel that takes the most device time in a second,
 profiled run of the same program (HIP events around every launch on the library's stream):
@@ -70,6 +71,7 @@ def gpu_run(prog, data, steps: int, warmup: int, graphs: bool = False):
     lib = hip.load(prog, seed=int(data.get("seed", 0)), graphs=graphs)
     # timed run
     lib.lib.anvil_marks_select(LOOP_COUNTER.encode())
+    lib.lib.anvil_marks_window(warmup, warmup + steps)     # events at the timed region's two ends only
     lib.lib.anvil_sync_device()
     t0 = time.perf_counter()
     with quiet_stdout():
@@ -171,6 +173,7 @@ def copy_run() -> dict:
     from anvil.backend import hip
     lib = hip.load(copy_program())
     lib.lib.anvil_marks_select(b"it")
+    lib.lib.anvil_marks_window(5, COPY_LAUNCHES - 1)
     with quiet_stdout():
         lib.main()
         lib.lib.anvil_sync_device()

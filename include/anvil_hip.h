@@ -78,8 +78,9 @@ double anvil_profile_bytes(int site);     /* algorithmic bytes of one launch (co
 /* ---- loop marks: a device event at the start of each iteration of the loops whose counter has
  * this name, for timing exactly K iterations. No counterpart in the reference. ---------------- */
 void anvil_marks_select(const char *counter_name);
+int anvil_marks_window(int first, int last);   /* events only at these two iterations; -1 if not 0 <= first <= last */
 int anvil_marks_count(void);
-double anvil_marks_elapsed_ms(int from_mark, int to_mark);
+double anvil_marks_elapsed_ms(int from_mark, int to_mark);   /* -1 where a mark has no event */
 
 /* ---- inspection ------------------------------------------------------------------------------ */
 /* Copy buffer `id` (its ir.Buffer.id) into dst; returns the bytes copied, -1 if the library holds

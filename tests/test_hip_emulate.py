@@ -77,3 +77,24 @@ def test_graph_mode_matches_reference(name):
     assert problem is None, problem
     for k in keep:
         assert tensors_match(z[f"buf:{k}"], arrays[k], rtol=1e-3) is None, k
+
+
+def test_loop_marks_window():
+    """The loop marks bench.py times with: every iteration of the selected loop counted, an event
+    only at the two iterations of the window, and no elapsed time for a mark outside it."""
+    from anvil.backend import hip
+    from fixtures import load_ir
+    prog, data = load_ir("c2_small")
+    src = hip.generate(prog, seed=data.get("seed", 0), emulate=True)
+    lib = hip.HipLibrary(hip.compile_source(src, emulate=True), src)
+    lib.lib.anvil_marks_select(b"x_batch")
+    assert lib.lib.anvil_marks_window(3, 1) == -1 and lib.lib.anvil_marks_window(-1, 4) == -1
+    assert lib.lib.anvil_marks_window(2, 9) == 0
+    assert lib.main() == 0
+    n = lib.lib.anvil_marks_count()
+    assert n == 41          # 32 batches of the first epoch, 9 of the second (the ninth breaks at STEPS = 40)
+    assert lib.lib.anvil_marks_elapsed_ms(2, 9) >= 0
+    assert lib.lib.anvil_marks_elapsed_ms(0, 9) == -1 and lib.lib.anvil_marks_elapsed_ms(2, 5) == -1
+    lib.lib.anvil_marks_select(b"x_batch")           # a new selection: every iteration again
+    assert lib.main() == 0
+    assert lib.lib.anvil_marks_count() == n and lib.lib.anvil_marks_elapsed_ms(0, n - 1) >= 0
