@@ -6,6 +6,11 @@ Run in the development container only (the reference checkout is not on the GPU 
 
 (--route-only: the IR and the reference-route source hashes, without running the interpreter.)
 
+The reference numbers IR objects from one counter per process (ir.py:37-41), so a program's ids
+depend on the programs compiled before it in the same run; a program marked `own_process` is
+written by a child process of its own, which gives it the same ids whether it is written alone or
+in a full run.
+
 For each program in `programs.py` (Anvil source written for this repository's tests and
 workloads) it writes:
   - ir/<name>.json       the optimized kernel IR that the reference front end produces
@@ -22,6 +27,7 @@ from __future__ import annotations
 import hashlib
 import importlib.util
 import io
+import subprocess
 import json
 import os
 import shutil
@@ -81,6 +87,14 @@ def main(ref_root: str) -> None:
     for spec in programs.PROGRAMS:
         name = spec["name"]
         if only and name not in only:
+            continue
+        if spec.get("own_process") and only != {name}:
+            with open(ROUTE, "w") as f:                  # what this run has so far, for the child to extend
+                json.dump(dict(sorted(route.items())), f, indent=1)
+            subprocess.run([sys.executable, os.path.abspath(__file__), ref_root, name]
+                           + (["--route-only"] if route_only else []), check=True)
+            with open(ROUTE) as f:
+                route[name] = json.load(f)[name]
             continue
         path = spec.get("path") or os.path.join(HERE, "programs", f"{name}.anvil")
         os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)

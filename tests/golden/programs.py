@@ -673,5 +673,5 @@ PROGRAMS = [
     # (0, 4), (1, 3) and the middle tile 2 alone, with all of a pair's key tiles staged at once
     {"name": "c4_t160", "source": C4,
      "consts": {"STEPS": 2, "BATCH": 2, "T": 160, "D": 128, "HEADS": 2, "LAYERS": 1}, "interp": True,
-     "keep": ["net.tok", "net.layers.0.Wqkv", "net.layers.0.Wout", "net.head.W"]},
+     "own_process": True, "keep": ["net.tok", "net.layers.0.Wqkv", "net.layers.0.Wout", "net.head.W"]},
 ]
