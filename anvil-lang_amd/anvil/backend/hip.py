@@ -115,6 +115,10 @@ class HipGen:
         self.check = check
         if check:
             graphs = False
+        # temporaries that are a cheap elementwise function of another buffer: recomputed where
+        # they are read (the CPU build too, so the CPU tests run the rewritten program)
+        if not check and os.environ.get("ANVIL_HIP_REMAT", "1") != "0":
+            prog = A.rematerialize(prog)
         if not emulate and not check and os.environ.get("ANVIL_HIP_SINK", "1") != "0":
             prog = A.sink_scalar_kernels(prog)
         if not emulate and not check and os.environ.get("ANVIL_HIP_GATHER_FWD", "1") != "0":

@@ -11,7 +11,10 @@
   needs no device round trip for its counters, its `if step >= N: break` or Adam's step count;
 - `plan_arena`: byte offsets of every device buffer in one allocation; temporaries whose lifetimes
   do not overlap share bytes (the reference's arena.py:1-144 lifetime rule: a lifetime that touches
-  a loop covers the whole loop, and only buffers whose first use writes all of them take part).
+  a loop covers the whole loop, and only buffers whose first use writes all of them take part);
+- `rematerialize`: temporaries that are a cheap elementwise function of another buffer (GELU's
+  tanh and 0.044715·x², which the reference's autodiff saves for the backward) recomputed where
+  they are read instead of written to and read back from memory.
 """
 from __future__ import annotations
 
@@ -348,6 +351,210 @@ def sink_scalar_kernels(prog: ir.Program) -> ir.Program:
     return dataclasses.replace(prog, main=block(prog.main))
 
 
+# ----------------------------------------------------------------------------- rematerialization
+
+REMAT_MAX_COST = 24     # recomputed per element read: a transcendental counts 8, any other op 1
+TRANSCENDENTAL = {"exp", "log", "sqrt", "tanh", "sigmoid", "sin", "cos", "rsqrt", "recip"}
+
+
+def _inline_lets(e):
+    """e with every Let reference replaced by the Let's (inlined) value."""
+    return ir.map_expr(e, lambda x: _inline_lets(x.let.value) if isinstance(x, ir.LetRef) else x)
+
+
+def _remat_cost(e) -> int:
+    n = 0
+    for x in ir.iter_expr(e):
+        if isinstance(x, ir.Unary):
+            n += 8 if x.op in TRANSCENDENTAL else (0 if x.op == "detach" else 1)
+        elif isinstance(x, (ir.Binary, ir.Select)):
+            n += 1
+    return n
+
+
+def _writers(prog: ir.Program) -> dict:
+    """buffer root id -> the statements (kernels, run-time calls, loop counters) that write it."""
+    out: dict[int, list] = {}
+
+    def walk(blk):
+        for st in blk.stmts:
+            if isinstance(st, ir.For):
+                out.setdefault(st.counter.root.id, []).append(st)
+                walk(st.body)
+            elif isinstance(st, ir.While):
+                walk(st.cond_block)
+                walk(st.body)
+            elif isinstance(st, ir.If):
+                walk(st.then)
+                walk(st.orelse)
+            else:
+                for b in stmt_writes(st):
+                    out.setdefault(b.id, []).append(st)
+    walk(prog.main)
+    return out
+
+
+def _blocks(blk):
+    yield blk
+    for st in blk.stmts:
+        if isinstance(st, ir.For):
+            yield from _blocks(st.body)
+        elif isinstance(st, ir.While):
+            yield from _blocks(st.cond_block)
+            yield from _blocks(st.body)
+        elif isinstance(st, ir.If):
+            yield from _blocks(st.then)
+            yield from _blocks(st.orelse)
+
+
+def _remat_candidate(prog: ir.Program, max_cost: int):
+    """The first (block, index of the writing kernel, its store, indices of the reading kernels)
+    whose temporary may be recomputed where it is read, or None.
+
+    Temporary T qualifies when: one kernel M writes it, with one plain store that covers every
+    element, whose value (Let references inlined) is built from constants and loads at the store's
+    own offset of buffers Z other than T (no loop index, random draw or reduction result), within
+    max_cost; each Z is written by one kernel that comes before M in the same block (so Z holds,
+    wherever T is read, the values M computed T from); and every statement that reads T is a kernel
+    after M in that block that reads it in values only (not as a gather index). T's element e is
+    then g(Z[e]), so a load T[o] can be replaced by g with each Z loaded at o. A T that some kernel
+    reads inside its reduction (an operand of a product) stays in memory."""
+    readers = all_readers(prog)
+    writers = _writers(prog)
+    for blk in _blocks(prog.main):
+        for i, st in enumerate(blk.stmts):
+            if not isinstance(st, KernelStmt):
+                continue
+            m = st.kernel
+            for s in m.stores:
+                t = s.buf
+                if t.root is not t or t.kind != "temp" or len(writers.get(t.id, ())) != 1:
+                    continue
+                if sum(1 for x in m.stores if x.buf.root is t) != 1 or not _store_covers(m, s, t):
+                    continue
+                g = _inline_lets(s.value)
+                if _remat_cost(g) > max_cost:
+                    continue
+                okey, ok, zs = s.offset.key(), True, set()
+                for x in ir.iter_expr(g):
+                    if isinstance(x, (ir.Index, ir.Rand, ir.Acc, ir.LetRef)):
+                        ok = False
+                    elif isinstance(x, Load):
+                        z = x.buf.root
+                        if x.offset.key() != okey or z is t or z in kernel_writes(m):
+                            ok = False
+                        else:
+                            zs.add(z)
+                    if not ok:
+                        break
+                if not ok or not zs:
+                    continue
+                for z in zs:
+                    w = writers.get(z.id, ())
+                    if len(w) != 1 or not any(w[0] is x for x in blk.stmts[:i]):
+                        ok = False
+                if not ok:
+                    continue
+                users = [j for j in range(i + 1, len(blk.stmts)) if isinstance(blk.stmts[j], KernelStmt)
+                         and t in kernel_reads(blk.stmts[j].kernel)]
+                if not users or readers.get(t.id, 0) != len(users):
+                    continue
+                for j in users:
+                    k = blk.stmts[j].kernel
+                    idx_loads = [ld for e in k.exprs() for ld in ir.loads_in(e)
+                                 for gth in ld.offset.gathers() if gth.load.buf.root is t]
+                    if idx_loads or any(gth.load.buf.root is t for x in k.stores for gth in x.offset.gathers()):
+                        ok = False
+                    # read inside a reduction (a product's operand), g would run once per term
+                    if k.red is not None and any(ld.buf.root is t for ld in ir.loads_in(k.red.body)):
+                        ok = False
+                if ok:
+                    return blk, i, s, users
+    return None
+
+
+def _substitute(k: ir.Kernel, t: Buffer, g, okey) -> ir.Kernel:
+    """Kernel k with each load of t at offset o replaced by g, its loads (at offset okey) moved to o."""
+    import dataclasses
+
+    def at(o):
+        def fn(x):
+            if isinstance(x, Load) and x.offset.key() == okey:
+                return Load(x.buf, o)
+            return x
+        return fn
+
+    lets: dict = {}
+
+    def fn(x):
+        if isinstance(x, Load) and x.buf.root is t:
+            return ir.map_expr(g, at(x.offset))
+        if isinstance(x, ir.LetRef) and x.let in lets:
+            return ir.LetRef(lets[x.let])
+        return x
+
+    stmts = []
+    for st in k.stmts:
+        if isinstance(st, ir.Let):
+            new = ir.Let(st.name, ir.map_expr(st.value, fn))
+            lets[st] = new
+            stmts.append(new)
+        else:
+            stmts.append(dataclasses.replace(st, value=ir.map_expr(st.value, fn)))
+    red = k.red
+    if red is not None:
+        red = dataclasses.replace(red, body=ir.map_expr(red.body, fn))
+    return dataclasses.replace(k, stmts=stmts, red=red)
+
+
+def rematerialize(prog: ir.Program, max_cost: int = REMAT_MAX_COST) -> ir.Program:
+    """The program with every temporary that `_remat_candidate` finds recomputed in the kernels that
+    read it, and its store dropped from the kernel that wrote it (the kernel itself too, if nothing
+    is left for it to store). The values are the same expressions of the same inputs, so with the
+    generated code's floating-point contraction off they are bit for bit what was stored before. The
+    caller's program is not changed."""
+    import dataclasses
+    for _ in range(10_000):
+        found = _remat_candidate(prog, max_cost)
+        if found is None:
+            break
+        blk, i, s, users = found
+        t, g, okey = s.buf, _inline_lets(s.value), s.offset.key()
+        stmts = list(blk.stmts)
+        for j in users:
+            stmts[j] = dataclasses.replace(stmts[j], kernel=_substitute(stmts[j].kernel, t, g, okey))
+        m = stmts[i].kernel
+        rest = [x for x in m.stmts if x is not s]
+        if any(isinstance(x, ir.Store) for x in rest):
+            stmts[i] = dataclasses.replace(stmts[i], kernel=dataclasses.replace(m, stmts=rest))
+        else:
+            del stmts[i]
+        prog = dataclasses.replace(prog, main=_replace_block(prog.main, blk, dataclasses.replace(blk, stmts=stmts)))
+    return prog
+
+
+def _replace_block(blk, old, new):
+    """blk with the block `old` (found by identity) replaced by `new`, copying the blocks on the way."""
+    import dataclasses
+    if blk is old:
+        return new
+    out, changed = [], False
+    for st in blk.stmts:
+        n = st
+        if isinstance(st, ir.For):
+            b = _replace_block(st.body, old, new)
+            n = st if b is st.body else dataclasses.replace(st, body=b)
+        elif isinstance(st, ir.While):
+            c, b = _replace_block(st.cond_block, old, new), _replace_block(st.body, old, new)
+            n = st if (c is st.cond_block and b is st.body) else dataclasses.replace(st, cond_block=c, body=b)
+        elif isinstance(st, ir.If):
+            a, b = _replace_block(st.then, old, new), _replace_block(st.orelse, old, new)
+            n = st if (a is st.then and b is st.orelse) else dataclasses.replace(st, then=a, orelse=b)
+        changed |= n is not st
+        out.append(n)
+    return dataclasses.replace(blk, stmts=out) if changed else blk
+
+
 # ----------------------------------------------------------------------------- program-wide reads
 
 def all_readers(prog: ir.Program) -> dict:
@@ -391,18 +598,18 @@ class ArenaPlan:
 
 def _full_write(k: ir.Kernel, b: Buffer) -> bool:
     """Does kernel k write every element of b (with plain stores)?"""
-    for st in k.stores:
-        if st.buf.root is not b or st.accumulate or st.offset.scalars() or st.offset.gathers():
-            continue
-        if st.offset.const != 0:
-            continue
-        n = ir.prod(v.extent for v in k.domain)
-        if n != b.numel or not injective_over(st.offset, k.domain):
-            continue
-        lo, hi = st.offset.var_bounds()
-        if lo == 0 and hi == b.numel - 1:
-            return True
-    return False
+    return any(st.buf.root is b and _store_covers(k, st, b) for st in k.stores)
+
+
+def _store_covers(k: ir.Kernel, st, b: Buffer) -> bool:
+    """Does store st of kernel k write every element of b, each once (a plain store)?"""
+    if st.accumulate or st.offset.scalars() or st.offset.gathers() or st.offset.const != 0:
+        return False
+    n = ir.prod(v.extent for v in k.domain)
+    if n != b.numel or not injective_over(st.offset, k.domain):
+        return False
+    lo, hi = st.offset.var_bounds()
+    return lo == 0 and hi == b.numel - 1
 
 
 def plan_arena(prog: ir.Program, device_bufs: list, full_writer, share: bool = True, fused=None,
