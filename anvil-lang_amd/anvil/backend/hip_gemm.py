@@ -528,13 +528,16 @@ class GemmPlan(Plan):
         self.ptm = self.ptn = 1             # 32 x 32 MFMA tiles per wavefront in the pipelined split
         # tuning: $ANVIL_GEMM_FORCE = comma-separated "tile64" | "tile128" | "ksplit:W:U" | "slab:KC" |
         # "kpipe:W:TM:TN", each optionally "@NN" / "@NT" / "@TN" (only products whose operands load
-        # that way)
+        # that way) or "@MxNxK" (only products of that shape)
         layout = {("ANVIL_LD_KC", "ANVIL_LD_RC"): "NN", ("ANVIL_LD_KC", "ANVIL_LD_KC"): "NT",
                   ("ANVIL_LD_RC", "ANVIL_LD_RC"): "TN"}.get((self.amode, self.bmode), "?")
+        shape = f"{s.M}x{s.N}x{s.K}"
+        self.forced = False
         for force in os.environ.get("ANVIL_GEMM_FORCE", "").split(","):
             force, _, only = force.partition("@")
-            if not force or (only and only != layout):
+            if not force or (only and only not in (layout, shape)):
                 continue
+            self.forced = True
             parts = force.split(":")
             if parts[0].startswith("tile"):
                 self.sched, self.BM = "tile", int(parts[0][4:])
@@ -553,7 +556,6 @@ class GemmPlan(Plan):
             if self.ptm * self.ptn == 1:
                 self.sched, self.BM, self.BN, self.slab, self.pipe, self.waves = "ksplit", 32, 32, 0, True, 4
             self.pipe = True
-        self.forced = any(f.partition("@")[0] for f in os.environ.get("ANVIL_GEMM_FORCE", "").split(","))
         self.followers = []             # (kernel, var map, forwarded loads) run in the epilogue
         self.layout()
 
@@ -619,10 +621,12 @@ class GemmPlan(Plan):
         them) win: the loaded operands serve TN (TM) products each and the wavefront carries
         independent accumulator chains. Measured (fp32, one MI355X): 8192 x 4096 x 4096 at 139
         TFLOP/s with one wavefront of 2 x 4 tiles (116 with the LDS-staged 128 x 128 tile); C4's
-        4096 x 1024 x 256 at 79-84 with 2 x 2 (68-73); 4096 x 256 x 1024 at 84 with four wavefronts
-        of 1 x 2 (77); batch-256 products stay at four wavefronts of one tile."""
+        4096 x 1024 x 256 at 79-84 with 2 x 2 (68-73); C4's 4096 x 256 x 1024 and 4096 x 256 x 768
+        products (forward and input gradients) 21-22 µs with four wavefronts of 2 x 2 against 25-27
+        with four of 1 x 2 (hipBLASLt: 18.6-22.1); batch-256 products stay at four wavefronts of
+        one tile."""
         s = self.s
-        for W, TM, TN, kmin in ((1, 2, 4, 0), (1, 2, 2, 0), (4, 1, 2, 512), (4, 1, 1, 0)):
+        for W, TM, TN, kmin in ((1, 2, 4, 0), (1, 2, 2, 0), (4, 2, 2, 512), (4, 1, 2, 512), (4, 1, 1, 0)):
             if -(-s.M // (32 * TM)) * -(-s.N // (32 * TN)) * s.B * W >= CU_WAVES and s.K >= kmin:
                 break
         self.sched, self.slab, self.pipe = "ksplit", 0, True

@@ -337,18 +337,27 @@ def c1_epoch(cpu: bool) -> dict:
     return out
 
 
-YARDSTICK_SHAPES = [(256, 1024, 784, "NN"), (256, 1024, 1024, "NN"), (256, 1024, 1024, "NT"),
-                    (784, 1024, 256, "TN"), (1024, 1024, 256, "TN")]
+YARDSTICK_SHAPES = {
+    # C2: fwd1, fwd2, dX2 and the weight gradients dW1, dW2 (M x N x K; TN: A stored K x M)
+    "c2": [(256, 1024, 784, "NN"), (256, 1024, 1024, "NN"), (256, 1024, 1024, "NT"),
+           (784, 1024, 256, "TN"), (1024, 1024, 256, "TN")],
+    # C4 at T = 256 (4096 tokens, width 256, feed-forward 1024): the forward products (qkv, attention
+    # output, feed-forward in and out), their input gradients and their weight gradients
+    "c4": [(4096, 768, 256, "NN"), (4096, 256, 256, "NN"), (4096, 1024, 256, "NN"), (4096, 256, 1024, "NN"),
+           (4096, 256, 768, "NT"), (4096, 256, 1024, "NT"), (4096, 1024, 256, "NT"),
+           (256, 768, 4096, "TN"), (256, 256, 4096, "TN"), (256, 1024, 4096, "TN"), (1024, 256, 4096, "TN")],
+}
 
 
-def yardstick(calls: int = 200) -> dict:
-    """The vendor library's fp32 products (torch.mm: hipBLASLt / rocBLAS, TF32 off) on C2's product
-    shapes, as a yardstick for the generated kernels. Event timing here includes the host's launch
-    rate; the kernels' own durations come from `rocprofv3 --kernel-trace --stats` of this mode."""
+def yardstick(config: str = "c2", calls: int = 200) -> dict:
+    """The vendor library's fp32 products (torch.mm: hipBLASLt / rocBLAS, TF32 off) on a config's
+    product shapes, as a yardstick for the generated kernels. Event timing here includes the host's
+    launch rate; the kernels' own durations come from `rocprofv3 --kernel-trace --stats` of this
+    mode."""
     import torch
     torch.backends.cuda.matmul.allow_tf32 = False
     out = []
-    for M, N, K, lay in YARDSTICK_SHAPES:
+    for M, N, K, lay in YARDSTICK_SHAPES[config]:
         a = torch.randn(*((K, M) if lay == "TN" else (M, K)), device="cuda")
         b = torch.randn(*((N, K) if lay == "NT" else (K, N)), device="cuda")
         c = torch.empty(M, N, device="cuda")
@@ -364,7 +373,8 @@ def yardstick(calls: int = 200) -> dict:
         e.record()
         torch.cuda.synchronize()
         out.append({"shape": f"{lay} {M}x{N}x{K}", "us_per_call_events": round(s.elapsed_time(e) / calls * 1e3, 2)})
-    return {"metric": "torch.mm fp32 on C2's product shapes (yardstick)", "calls": calls, "products": out}
+    return {"metric": f"torch.mm fp32 on {config.upper()}'s product shapes (yardstick)", "calls": calls,
+            "products": out}
 
 
 def main() -> int:
@@ -379,7 +389,8 @@ def main() -> int:
     p.add_argument("--graphs", action="store_true", help="replay loop bodies as HIP graphs")
     p.add_argument("--copy", action="store_true", help="run the copy kernel that calibrates HBM counters")
     p.add_argument("--c3", action="store_true", help="config C3: the standalone functions, per kernel")
-    p.add_argument("--yardstick", action="store_true", help="torch.mm (the vendor library) on C2's product shapes")
+    p.add_argument("--yardstick", nargs="?", const="c2", choices=sorted(YARDSTICK_SHAPES),
+                   help="torch.mm (the vendor library) on a config's product shapes (default c2)")
     p.add_argument("--oracle-leg", nargs=3, metavar=("IR", "COUNTER", "STOP"), help=argparse.SUPPRESS)
     args = p.parse_args()
     if args.oracle_leg:
@@ -387,7 +398,7 @@ def main() -> int:
         print(json.dumps(oracle_leg(path, counter, int(stop) or None)), flush=True)
         return 0
     if args.yardstick:
-        print(json.dumps(yardstick()), flush=True)
+        print(json.dumps(yardstick(args.yardstick)), flush=True)
         return 0
     if args.copy:
         print(json.dumps(copy_run()), flush=True)
