@@ -313,6 +313,9 @@ class HipGen:
             scat = HK.scatter_targets(k)
             if scat is not None:
                 return HK.GatherSumPlan(self, k, name, *scat), 1
+            rows = None if self.emulate or self.check else HK.index_scatter(k)
+            if rows is not None and os.environ.get("ANVIL_HIP_INDEX_SCATTER", "1") != "0":
+                return HK.IndexScatterPlan(self, k, name, *rows), 1
             return HK.MapPlan(self, k, name), 1
         if self.gemm is not None:
             g = self.gemm.match(self, k, name)

@@ -61,18 +61,29 @@ def program_max_id(prog: ir.Program) -> int:
     return top
 
 
+def _numbered(make, ident: int):
+    """make() (an IR constructor call) given the id `ident`, without drawing from the IR module's
+    id counter: the constructors take their id from the module's fresh_id, which is replaced by a
+    stand-in while they run (generation is single-threaded). Objects the front end numbers later
+    in the same process then get the ids they would have got without this generation."""
+    saved = ir.fresh_id
+    ir.fresh_id = lambda: ident
+    try:
+        obj = make()
+    finally:
+        ir.fresh_id = saved
+    obj.id = ident
+    return obj
+
+
 def new_var(ident: int, name: str, extent: int) -> Var:
-    """A loop variable with a chosen id (built with the IR's own constructor, then renumbered)."""
-    v = Var(name, extent)
-    v.id = ident
-    return v
+    """A loop variable with a chosen id (built with the IR's own constructor)."""
+    return _numbered(lambda: Var(name, extent), ident)
 
 
 def new_buffer(ident: int, name: str, shape, dtype: str, kind: str) -> Buffer:
     """A buffer of the backend's own (scratch, host-scalar copies) with a fixed id."""
-    b = Buffer(name, shape, dtype, kind)
-    b.id = ident
-    return b
+    return _numbered(lambda: Buffer(name, shape, dtype, kind), ident)
 
 
 def rt_args(st, table) -> list:

@@ -459,6 +459,173 @@ class GatherSumPlan(Plan):
         return self.blocks, THREADS
 
 
+# ----------------------------------------------------------------------------- index scatter
+
+INDEX_SCATTER_MAX_POS = 8192        # positions a workgroup's lanes hold in registers while they scan
+INDEX_SCATTER_MAX_ROWS = 1024       # every workgroup scans every position: R x P index loads
+
+
+def index_scatter(k: ir.Kernel):
+    """For a `+=` into rows of a small table picked by an index array (an embedding's gradient:
+    dE[tok[n, t], d] += dX[n, t, d]): (column vars, position vars, the gather, row width W, rows R,
+    positions P), or None. The store's offset is W·idx[...] plus a row-major index over [0, W) of
+    the column variables, which the index load does not use; the other domain variables are the
+    positions. Only where positions collide (P >= 2R, a few rows, a bounded scan)."""
+    if k.red is not None or k.uses_rand() or not k.domain or len(k.stores) != 1:
+        return None
+    if not all(isinstance(x, (ir.Let, ir.Store)) for x in k.stmts):
+        return None
+    st = k.stores[0]
+    off = st.offset
+    if not st.accumulate or st.buf.dtype != F32 or off.const != 0 or off.scalars() or len(off.gathers()) != 1:
+        return None
+    g = off.gathers()[0]
+    W = off.coef(g)
+    if W <= 0 or g.rest is not None or g.load.offset.gathers() or g.load.offset.scalars():
+        return None
+    cols = sorted((v for v in off.terms if isinstance(v, Var)), key=lambda v: -off.coef(v))
+    if any(v not in k.domain for v in cols) or ir.prod(v.extent for v in cols) != W:
+        return None
+    stride = W
+    for v in cols:
+        stride //= v.extent
+        if off.coef(v) != stride:
+            return None
+    if any(g.load.offset.coef(v) for v in cols):
+        return None
+    if any(ld.buf.root is st.buf.root for ld in A.kernel_loads(k)):
+        return None
+    pos = [v for v in k.domain if v not in cols]
+    P = ir.prod(v.extent for v in pos)
+    lo, R = g.check_range()
+    if lo != 0 or not 0 < R <= INDEX_SCATTER_MAX_ROWS or P > INDEX_SCATTER_MAX_POS or P < 2 * R:
+        return None
+    if R * W > st.buf.root.numel:
+        return None
+    return cols, pos, g, W, R, P
+
+
+class IndexScatterPlan(Plan):
+    """The `+=` of `index_scatter` without atomics: one workgroup per table row r. Its four
+    wavefronts each scan a quarter of the positions (the index loads, with their bounds check, in
+    registers); a ballot per 64 positions counts those whose index is r, and once the wavefronts'
+    counts are known each writes its hits, in position order, into one list in LDS. Then each lane
+    takes a column of the row and adds the listed positions' values to the table's element in
+    list order (the order of the sequential `+=`), BATCH positions' loads in flight at a time, and
+    writes the element once."""
+
+    kind = "index-scatter"
+    BATCH = 16
+
+    def __init__(self, gen, k, name, cols, pos, g, W, R, P):
+        super().__init__(gen, [k], name)
+        self.k = k
+        self.cols, self.pos, self.g, self.W, self.R, self.P = cols, pos, g, W, R, P
+        self.S = -(-P // THREADS)                    # positions per lane in the scan
+        self.Q = 64 * self.S                         # positions per wavefront
+        self.blocks = R
+        self.batch = int(os.environ.get("ANVIL_SCATTER_BATCH", str(self.BATCH)))
+
+    def source(self) -> str:
+        k, st = self.k, self.k.stores[0]
+        T, S, Q, P, W, R, B = THREADS, self.S, self.Q, self.P, self.W, self.R, self.batch
+        sc = KernelScope(self)
+        sc.stream_name = self.stream_param(k)
+        body: list[str] = []
+        em = Emitter(sc, body, "        ")
+        # the index loads first, all in flight, then their bounds checks (a check's branch to the
+        # fault report between two loads would hold the second back until the first arrives)
+        g = self.g
+        lo, hi = g.check_range()
+        code = sc.fault(f"index out of bounds ({g.where or 'gather'}; dimension size {g.bound})")
+        em.emit(f"int idx_[{S}];")
+        em.emit("#pragma unroll")
+        em.emit(f"for (int s = 0; s < {S}; s++) {{")
+        em.emit(f"    const uint32_t p = wave * {Q}u + 64u * (uint32_t)s + lane;")
+        em.emit(f"    idx_[s] = {ilit(lo)};")
+        em.emit(f"    if (p < {P}u) {{")
+        em.ind += "        "
+        for line in decode(self.pos, "p", "uint32_t"):
+            em.emit(line)
+        em.emit(f"idx_[s] = {em.ex(g.load)};")
+        em.ind = em.ind[:-8]
+        em.emit("    }")
+        em.emit("}")
+        em.reset_memo()
+        em.emit("#pragma unroll")
+        em.emit(f"for (int s = 0; s < {S}; s++) {{")
+        em.emit(f"    if (idx_[s] < {ilit(lo)} || idx_[s] >= {ilit(hi)}) {{ anvil_fault({code}, idx_[s]); idx_[s] = {ilit(lo)}; }}")
+        em.emit(f"    if (wave * {Q}u + 64u * (uint32_t)s + lane >= {P}u) idx_[s] = -1;      // past the last position")
+        em.emit("}")
+        em.emit("int cnt = 0;")
+        em.emit("#pragma unroll")
+        em.emit(f"for (int s = 0; s < {S}; s++) cnt += __popcll(__ballot(idx_[s] == (int)row));")
+        em.emit("if (lane == 0) anvil_nhit[wave] = cnt;")
+        em.emit("__syncthreads();")
+        em.emit("int base = 0;")
+        em.emit("for (uint32_t w = 0; w < wave; w++) base += anvil_nhit[w];")
+        em.emit("const int nh = anvil_nhit[0] + anvil_nhit[1] + anvil_nhit[2] + anvil_nhit[3];")
+        em.emit("#pragma unroll")
+        em.emit(f"for (int s = 0; s < {S}; s++) {{")
+        em.emit("    const unsigned long long m = __ballot(idx_[s] == (int)row);")
+        em.emit("    if (idx_[s] == (int)row)")
+        em.emit(f"        anvil_hits[base + __popcll(m & ((1ull << lane) - 1ull))] = "
+                f"(int)(wave * {Q}u + 64u * (uint32_t)s + lane);")
+        em.emit("    base += __popcll(m);")
+        em.emit("}")
+        em.emit("__syncthreads();")
+        rv = A.new_var(900_000_200, "r", R)
+        em.emit(f"const int v{rv.id} = (int)row;")
+        em.emit(f"for (uint32_t col = threadIdx.x; col < {W}u; col += {T}u) {{")
+        em.ind += "    "
+        for line in decode(self.cols, "col", "uint32_t"):
+            em.emit(line)
+        target_off = ir.Affine(0, {rv: W, **{v: st.offset.coef(v) for v in self.cols}})
+        target = f"{sc.buf(st.buf)}[{em.affine(target_off, st.buf)}]"
+        em.emit(f"float acc = {target};")
+        em.emit(f"for (int h0 = 0; h0 < nh; h0 += {B}) {{")
+        em.ind += "    "
+        em.emit(f"float x_[{B}];")
+        saved = em.memo
+        for j in range(B):
+            em.emit(f"x_[{j}] = 0.0f;")
+            em.emit(f"if (h0 + {j} < nh) {{")
+            em.ind += "    "
+            em.emit(f"const uint32_t p = (uint32_t)anvil_hits[h0 + {j}];")
+            em.memo = dict(saved)
+            for line in decode(self.pos, "p", "uint32_t"):
+                em.emit(line)
+            val = None
+            for stmt in k.stmts:
+                if isinstance(stmt, ir.Let):
+                    em.let(stmt)
+                else:
+                    val = em.store_value(stmt)
+            em.emit(f"x_[{j}] = {val};")
+            em.ind = em.ind[:-4]
+            em.emit("}")
+        em.memo = saved
+        em.emit("#pragma unroll")
+        em.emit(f"for (int j = 0; j < {B}; j++)")
+        em.emit("    if (h0 + j < nh) acc += x_[j];")
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        em.emit(f"{target} = acc;")
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        em.emit("__syncthreads();")
+        head = [self.comment() + f" · one workgroup per table row ({R} rows of {W}), {P} positions scanned in order",
+                self.header(T),
+                f"    __shared__ int anvil_hits[{4 * Q}];",
+                "    __shared__ int anvil_nhit[4];",
+                "    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;",
+                f"    for (uint32_t row = blockIdx.x; row < {R}u; row += gridDim.x) {{"]
+        return "\n".join(head + body + ["    }", "}"])
+
+    def grid(self):
+        return self.blocks, THREADS
+
+
 # ----------------------------------------------------------------------------- serial
 
 class SerialPlan(Plan):
