@@ -1474,6 +1474,27 @@ class RowBlockPlan(Plan):
     def grid(self):
         return self.blocks, self.threads
 
+    def row_owned(self, b) -> bool:
+        """Does each element of buffer b belong to one lane of one row's workgroup, so that a `+=`
+        to it needs no atomic? Every store of the launch to b is at the row-major index of its
+        kernel's domain, which is b's size: row r then writes only its own slice of b, one lane per
+        element within a stage, and the workgroup's barriers between stages order the stages."""
+        for k in self.kernels:
+            for o in k.stores:
+                if o.buf.root is not b:
+                    continue
+                off = o.offset
+                if off.gathers() or off.scalars() or off.const != 0 or len(off.terms) != len(k.domain):
+                    return False
+                if ir.prod(v.extent for v in k.domain) != b.numel:
+                    return False
+                stride = 1
+                for v in reversed(k.domain):
+                    if off.coef(v) != stride:
+                        return False
+                    stride *= v.extent
+        return True
+
     def stage_statements(self, em, k, sc, guard=None):
         for st in k.stmts:
             if isinstance(st, ir.Let):
@@ -1488,7 +1509,14 @@ class RowBlockPlan(Plan):
                 lines.append(f"atomicAdd(&{sh}, {val});" if st.accumulate else f"{sh} = {val};")
             if b.id not in self.dead:
                 target = f"{sc.buf(st.buf)}[{off}]"
-                lines.append(f"atomicAdd(&{target}, {val});" if st.accumulate else f"{target} = {val};")
+                if not st.accumulate:
+                    lines.append(f"{target} = {val};")
+                elif not self.row_owned(b):
+                    lines.append(f"atomicAdd(&{target}, {val});")
+                elif b.dtype == I32:
+                    lines.append(f"{target} = anvil_wrap_add({target}, {val});")
+                else:
+                    lines.append(f"{target} += {val};")
             for line in lines:
                 em.emit(f"if ({guard}) {line}" if guard else line)
             em.reset_memo()
