@@ -674,4 +674,16 @@ PROGRAMS = [
     {"name": "c4_t160", "source": C4,
      "consts": {"STEPS": 2, "BATCH": 2, "T": 160, "D": 128, "HEADS": 2, "LAYERS": 1}, "interp": True,
      "own_process": True, "keep": ["net.tok", "net.layers.0.Wqkv", "net.layers.0.Wout", "net.head.W"]},
+    # a `+=` into table rows picked by an index array at sizes the C4 fixtures do not reach: more
+    # columns than a workgroup has lanes, positions not a multiple of 256, an odd number of rows
+    {"name": "scatter_rows", "interp": True, "own_process": True, "keep": ["G", "S"], "source": """
+tok: i32[9, 111] ~ randint(0, 7)
+X: [9, 111, 300] ~ normal(0, 1)
+G: [7, 300] = 0.0
+G[tok[n, t], d] += X[n, t, d]
+S: [7, 300] = 0.0
+S[tok[n, t], d] += X[n, t, d] * 2.0 - 1.0
+print(G[0:2])
+print(S[5:7])
+"""},
 ]

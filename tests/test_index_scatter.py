@@ -3,7 +3,8 @@ small table picked by an index array, run without atomics, one workgroup per tab
 
 Which kernels take it, and the kernel it generates, are checked here; the results are checked on
 the GPU against the reference's vectors by the programs that use it (the `scatter` fixture's
-histogram, C4's token-embedding gradient in c4_t160, c4_full2 and c4_t256_2).
+histogram; `scatter_rows`: 300 columns, more than a workgroup's lanes, 999 positions, 7 rows; C4's
+token-embedding gradient in c4_t160, c4_full2 and c4_t256_2).
 """
 import re
 
@@ -62,7 +63,7 @@ def test_column_used_by_the_index_is_rejected():
     assert HK.index_scatter(_scatter_kernel(col_in_index=True)) is None
 
 
-@pytest.mark.parametrize("name", ["c4_t160", "scatter"])
+@pytest.mark.parametrize("name", ["c4_t160", "scatter", "scatter_rows"])
 def test_generated_kernel(name):
     """The generated kernel: no atomics, the bounds check kept in the scan, the LDS list sized for
     every position, and the adds in list order."""
