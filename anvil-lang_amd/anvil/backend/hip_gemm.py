@@ -572,7 +572,8 @@ class GemmPlan(Plan):
         # the epilogue (see GemmReducePlan)
         tiles = -(-s.M // self.BM) * -(-s.N // self.BN) * s.B if self.pipe else -(-s.M // 32) * -(-s.N // 32) * s.B
         self.kslices, self.kslice = 1, s.K
-        if (self.pipe and tiles * self.waves < CU_WAVES // 2 and s.K >= 4096
+        if (self.pipe and tiles * self.waves < CU_WAVES // 2
+                and s.K >= int(os.environ.get("ANVIL_GEMM_SPLITK_MINK", "4096"))
                 and os.environ.get("ANVIL_GEMM_SPLITK", "1") != "0"):
             S = max(2, min(1024 // tiles, s.K // 512))
             self.kslice = -(-(-(-s.K // S)) // 8) * 8
