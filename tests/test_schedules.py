@@ -1,0 +1,57 @@
+"""Schedule choices that the measurements fixed, pinned on the generated source (CPU).
+
+- four wavefronts of 2 x 2 MFMA tiles for C4's tall N = 256 products with K >= 512 (a 64 x 64
+  output tile per workgroup), while C2's batch-256 products keep four wavefronts of one tile;
+- `ANVIL_GEMM_FORCE=<schedule>@MxNxK` changes the products of that shape only;
+- row blocks of more than 2048 rows run with 128 lanes per row, shorter ones with 256.
+"""
+import re
+
+from fixtures import load_ir
+
+from anvil.backend import hip
+
+
+def _source(name):
+    prog, data = load_ir(name)
+    return hip.generate(prog, seed=data.get("seed", 0))
+
+
+def _schedules(src):
+    """shape -> set of schedule strings of its products ('ksplit 64x64', 'tile 64x64', ...)."""
+    out: dict = {}
+    for shape, sched in re.findall(r"^// gemm: .*· (\d+x\d+x\d+) · (ksplit \d+x\d+|tile \d+x\d+)", src, re.M):
+        out.setdefault(shape, set()).add(sched)
+    return out
+
+
+def test_tall_products_take_two_by_two_tiles():
+    s = _schedules(_source("c4_t256_2"))
+    assert s["4096x256x1024"] == {"ksplit 64x64"} and s["4096x256x768"] == {"ksplit 64x64"}
+    # K = 256: four wavefronts of one tile, K split four ways
+    assert s["4096x256x256"] == {"ksplit 32x32"}
+
+
+def test_batch_256_products_keep_one_tile_per_wavefront():
+    s = _schedules(_source("c2_wide_mlp"))
+    assert s["256x1024x1024"] == {"ksplit 32x32"}
+
+
+def test_force_by_shape_touches_that_shape_only(monkeypatch):
+    base = _schedules(_source("c4_t256_2"))
+    monkeypatch.setenv("ANVIL_GEMM_FORCE", "tile64@4096x256x256")
+    forced = _schedules(_source("c4_t256_2"))
+    assert forced["4096x256x256"] == {"tile 64x64"}
+    assert {k: v for k, v in forced.items() if k != "4096x256x256"} == \
+           {k: v for k, v in base.items() if k != "4096x256x256"}
+
+
+def _rowblock_lanes(src):
+    return {(int(rows), int(lanes)) for rows, lanes in re.findall(
+        r"rowblock: .*· one workgroup per row, (\d+) rows\n__global__ void __launch_bounds__\((\d+)\)", src)}
+
+
+def test_rowblock_lanes_follow_the_row_count():
+    assert _rowblock_lanes(_source("c4_t256_2")) == {(4096, 128)}
+    assert _rowblock_lanes(_source("c2_wide_mlp")) == {(256, 256)}
+    assert {lanes for _, lanes in _rowblock_lanes(_source("c4_full2"))} == {256}      # 1024 rows
