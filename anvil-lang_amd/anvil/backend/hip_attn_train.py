@@ -36,6 +36,8 @@ from __future__ import annotations
 
 import os
 
+import numpy as np
+
 from .. import ir
 from ..ir import Binary, KernelStmt, Load, Unary
 from . import hip_analysis as A
@@ -286,6 +288,26 @@ def _vars4(k: ir.Kernel, red_extent: int):
     return list(k.domain), k.red.vars[0]
 
 
+def _slices_tile(sh: _Shape, numel: int) -> bool:
+    """Do the Q, K and V slices of QKV cover each of its numel elements exactly once? The fused
+    backward writes dQ, dK and dV with plain stores at those offsets of G (same layout as QKV) in
+    place of the chain's `G = 0` and its three `+=`: with two slices at one place (Q and K read
+    from the same columns) their gradients would overwrite each other instead of adding, and an
+    element no slice covers (a fourth, unused slice) would keep stale memory instead of 0."""
+    B, H, T, D = sh.B, sh.H, sh.T, sh.D
+    rel = (np.arange(B, dtype=np.int64)[:, None, None, None] * sh.qn
+           + np.arange(H, dtype=np.int64)[None, :, None, None] * sh.qh
+           + np.arange(T, dtype=np.int64)[None, None, :, None] * sh.qs
+           + np.arange(D, dtype=np.int64)[None, None, None, :]).reshape(-1)
+    hits = np.zeros(numel, dtype=np.int64)
+    for base in (sh.q0, sh.k0, sh.v0):
+        at = rel + base
+        if at.min() < 0 or at.max() >= numel:
+            return False
+        hits += np.bincount(at, minlength=numel)
+    return bool((hits == 1).all())
+
+
 def _backward(gen, stmts: list, j: int, sh: _Shape):
     """The eight backward kernels at stmts[j:j+8] for the forward described by sh, or None."""
     if j + 8 > len(stmts) or not all(isinstance(st, KernelStmt) for st in stmts[j:j + 8]):
@@ -303,7 +325,7 @@ def _backward(gen, stmts: list, j: int, sh: _Shape):
     G = sts[0].buf.root
     if not (isinstance(cv, ir.Const) and cv.value == 0.0) or not A._full_write(k0, G) or G.dtype != ir.F32:
         return None
-    if G.numel != sh.QKV.numel or G is sh.QKV:
+    if G.numel != sh.QKV.numel or G is sh.QKV or not _slices_tile(sh, G.numel):
         return None
     # G[V] += Σ_t dO · P
     got = _vars4(k1, T)

@@ -34,6 +34,10 @@ MAX_BLOCKS = 1 << 16
 QMAX = 16                       # register-cached elements per lane and row
 CACHE_REGS = 96                 # register budget for cached row elements, per lane
 CU_WAVES = 256 * 4              # waves that fill the chip once (256 CUs x 4 SIMDs)
+# The interpreter evaluates a reduction with no output index over more than CHUNK elements in
+# chunks of its first reduction variable (interp.py:25, 392-406, 484-516); argmax / argmin combine
+# the chunks' picks by a rule of their own (arg_chunk).
+CHUNK = 1 << 22
 
 
 def index_type(n: int) -> str:
@@ -111,6 +115,24 @@ def red_combine(op: str, dtype: str, a: str, b: str) -> str:
 
 
 RED_CODE = {"sum": "ANVIL_RED_SUM", "prod": "ANVIL_RED_PROD", "max": "ANVIL_RED_MAX", "min": "ANVIL_RED_MIN"}
+
+
+def arg_pick(op: str, val: str, idx: str, best: str, at: str) -> str:
+    """C that lets element (val, idx) replace the running argmax / argmin pick (best, at)."""
+    mx = "true" if op == "argmax" else "false"
+    return f"if (anvil_arg_better<{mx}>({val}, {idx}, {best}, {at})) {{ {best} = {val}; {at} = {idx}; }}"
+
+
+def arg_chunk(k: ir.Kernel) -> int:
+    """Elements per interpreter chunk for an argmax / argmin with no output index over more than
+    CHUNK elements (0: evaluated whole): ranges of `per` values of the first reduction variable."""
+    if k.red is None or k.red.op not in ("argmax", "argmin") or k.domain:
+        return 0
+    n = ir.prod(v.extent for v in k.red.vars)
+    if n <= CHUNK:
+        return 0
+    inner = n // k.red.vars[0].extent
+    return max(1, CHUNK // max(1, inner)) * inner
 
 
 class KernelScope(Scope):
@@ -662,8 +684,12 @@ def serial_reduction(em: Emitter, sc: KernelScope, k: ir.Kernel, ind: str, unrol
     op, dt = red.op, red.body.dtype
     T = ctype(dt)
     arg = op in ("argmax", "argmin")
+    P = arg_chunk(k)
+    n = ir.prod(v.extent for v in red.vars)
     if arg:
         em.emit(f"{T} best = {red_init(op, dt)}; int acc = 2147483647; int ridx = 0;")
+        if P:
+            em.emit(f"{T} cbest = {red_init(op, dt)}; int cat = 2147483647;")
     else:
         em.emit(f"{T} acc = {red_init(op, dt)};")
     saved_ind = em.ind
@@ -675,9 +701,17 @@ def serial_reduction(em: Emitter, sc: KernelScope, k: ir.Kernel, ind: str, unrol
     saved = em.memo
     em.memo = dict(saved)
     val = em.ex(red.body)
-    if arg:
-        em.emit(f"if ({val} {'>' if op == 'argmax' else '<'} best || ({val} == best && ridx < acc)) "
-                f"{{ best = {val}; acc = ridx; }}")
+    if arg and P:
+        # one lane walks the elements in order: close each interpreter chunk as it ends
+        em.emit(arg_pick(op, val, "ridx", "cbest", "cat"))
+        em.emit("ridx++;")
+        em.emit(f"if (ridx % {P} == 0 || ridx == {n}) {{")
+        em.emit(f"    if (ridx <= {P} || anvil_chunk_better<{'true' if op == 'argmax' else 'false'}>(cbest, best)) "
+                "{ best = cbest; acc = cat; }")
+        em.emit(f"    cbest = {red_init(op, dt)}; cat = 2147483647;")
+        em.emit("}")
+    elif arg:
+        em.emit(arg_pick(op, val, "ridx", "best", "acc"))
         em.emit("ridx++;")
     else:
         em.emit(f"acc = {red_combine(op, dt, 'acc', val)};")
@@ -904,30 +938,71 @@ class RowsPlan(Plan):
             em.emit(f"{T} best{si} = {red_init(op, dt)}; int acc{si} = 2147483647;")
         else:
             em.emit(f"{T} acc{si} = {red_init(op, dt)};")
+        mx = "true" if op == "argmax" else "false"
+        if arg and arg_chunk(k):
+            self.chunked_arg_stage(em, sc, k, si, shared, arg_chunk(k))
+            sc.acc_name = f"acc{si}"
+            sc.fwd = dict(fwd)
+            self.row_statements(em, sc, k, cm, fwd)
+            return
 
         def body():
             val = em.ex(red.body)
             if arg:
-                em.emit(f"if ({val} {'>' if op == 'argmax' else '<'} best{si} || ({val} == best{si} && (int)j < acc{si})) "
-                        f"{{ best{si} = {val}; acc{si} = (int)j; }}")
+                em.emit(arg_pick(op, val, "(int)j", f"best{si}", f"acc{si}"))
             else:
                 em.emit(f"acc{si} = {red_combine(op, dt, f'acc{si}', val)};")
         self.element_loop(em, list(red.vars), body)
         if self.L == 64:
             if arg:
-                em.emit(f"anvil_wave_arg<{'true' if op == 'argmax' else 'false'}, {T}>(best{si}, acc{si});")
+                em.emit(f"anvil_wave_arg<{mx}, {T}>(best{si}, acc{si});")
             else:
                 em.emit(f"acc{si} = anvil_wave_all<{RED_CODE[op]}, {T}>(acc{si});")
         elif self.L == THREADS:
             if arg:
                 shared.append(f"    __shared__ {T} sv{si}[4]; __shared__ int si{si}[4];")
-                em.emit(f"anvil_block_arg<{'true' if op == 'argmax' else 'false'}, {T}>(best{si}, acc{si}, sv{si}, si{si});")
+                em.emit(f"anvil_block_arg<{mx}, {T}>(best{si}, acc{si}, sv{si}, si{si});")
             else:
                 shared.append(f"    __shared__ {T} sv{si}[4];")
                 em.emit(f"acc{si} = anvil_block_all<{RED_CODE[op]}, {T}>(acc{si}, sv{si});")
         sc.acc_name = f"acc{si}"
         sc.fwd = dict(fwd)
         self.row_statements(em, sc, k, cm, fwd)
+
+    def chunked_arg_stage(self, em, sc, k, si, shared, P: int):
+        """argmax / argmin with no output index over more than CHUNK elements: the row's lanes pick
+        within each interpreter chunk of P elements (nan first, then the extreme, ties to the
+        smaller index), combine the chunk's pick across the lanes, and the chunk picks meet in
+        chunk order by the interpreter's rule (anvil_chunk_better)."""
+        red = k.red
+        op, dt = red.op, red.body.dtype
+        T = ctype(dt)
+        mx = "true" if op == "argmax" else "false"
+        L, n = self.L, self.n
+        em.emit(f"for (uint32_t c0 = 0; c0 < {n}u; c0 += {P}u) {{")
+        em.ind += "    "
+        em.emit(f"const uint32_t c1 = c0 + {P}u < {n}u ? c0 + {P}u : {n}u;")
+        em.emit(f"{T} cb = {red_init(op, dt)}; int ca = 2147483647;")
+        em.emit(f"for (uint32_t j = c0 + (uint32_t)lane; j < c1; j += {L}u) {{")
+        em.ind += "    "
+        saved_memo = em.memo
+        em.memo = dict(saved_memo)
+        for line in decode(list(red.vars), "j", "uint32_t"):
+            em.emit(line)
+        val = em.ex(red.body)
+        em.emit(arg_pick(op, val, "(int)j", "cb", "ca"))
+        em.memo = saved_memo
+        em.ind = em.ind[:-4]
+        em.emit("}")
+        if L == 64:
+            em.emit(f"anvil_wave_arg<{mx}, {T}>(cb, ca);")
+        elif L == THREADS:
+            shared.append(f"    __shared__ {T} sv{si}[4]; __shared__ int si{si}[4];")
+            em.emit(f"anvil_block_arg<{mx}, {T}>(cb, ca, sv{si}, si{si});")
+            em.emit("__syncthreads();                  // the slots are written again for the next chunk")
+        em.emit(f"if (c0 == 0 || anvil_chunk_better<{mx}>(cb, best{si})) {{ best{si} = cb; acc{si} = ca; }}")
+        em.ind = em.ind[:-4]
+        em.emit("}")
 
     def row_statements(self, em, sc, k, cm, fwd):
         def on_store(st, val):
@@ -1291,7 +1366,7 @@ class RowBlockPlan(Plan):
     FORWARD_REGS = 64               # registers per lane holding operands forwarded between stages
     HOIST = 8                       # per-row operand loads issued before the first stage
 
-    def __init__(self, gen, kernels, name, R: int):
+    def __init__(self, gen, kernels, name, R: int, before: set = frozenset()):
         super().__init__(gen, kernels, name)
         self.R = R
         # 256 lanes per row, or 128 when there are more rows than 256-lane workgroups fit on the
@@ -1300,6 +1375,7 @@ class RowBlockPlan(Plan):
         self.threads = int(os.environ.get("ANVIL_ROWBLOCK_THREADS", "128" if R > 2048 else str(THREADS)))
         self.blocks = min(R, MAX_BLOCKS)
         self.shadow: dict = {}      # buffer id -> row slice (kept in LDS)
+        self.before_ids = set(before)
         self.dead: set = set()      # buffers only the chain reads: no memory copy
         readers_in: dict = {}
         for k in kernels:
@@ -1312,6 +1388,11 @@ class RowBlockPlan(Plan):
                 if b.id in self.shadow:
                     continue
                 S = b.numel // R
+                # a buffer some stage reads before the chain writes it (`before`: the values of a
+                # kernel ahead of the launch, or the target of a `+=`) keeps its memory copy as the
+                # only one: an LDS shadow starts empty, so those reads would see no values
+                if b.id in before:
+                    continue
                 dead = (b.kind in A.SHARED_KINDS and not gen.is_host(b) and not getattr(b, "heap", False)
                         and gen.readers.get(b.id, 0) == readers_in.get(b.id, 0))
                 accum = any(s2.accumulate and s2.buf.root is b for k2 in kernels for s2 in k2.stores)
@@ -2012,8 +2093,6 @@ class GroupBuilder:
             return False
         if k.red is not None:
             if [v.extent for v in k.domain] != self.outer_ext or [v.extent for v in k.red.vars] != self.inner_ext:
-                return False
-            if k.red.op in ("argmax", "argmin") and False:
                 return False
         else:
             no = len(self.outer_ext)

@@ -82,6 +82,28 @@ ANVIL_HD static inline float anvil_maxf(float a, float b) { return (a != a) ? a 
 ANVIL_HD static inline float anvil_minf(float a, float b) { return (a != a) ? a : (b != b) ? b : (b < a ? b : a); }
 ANVIL_HD static inline int anvil_maxi(int a, int b) { return a < b ? b : a; }
 ANVIL_HD static inline int anvil_mini(int a, int b) { return b < a ? b : a; }
+// argmax / argmin as np.argmax / np.argmin pick (interp.py:478-481): a nan beats every number and
+// the first nan wins; among numbers the strictly larger (smaller) value, a tie to the smaller index.
+// Does element (v, i) replace the running pick (best, at)? The relation orders (value, index)
+// pairs totally, so partial picks may meet in any order (lane loops, wavefront and LDS trees).
+template <bool MAX> ANVIL_HD static inline bool anvil_arg_better(float v, int i, float best, int at) {
+    const bool vn = v != v, bn = best != best;
+    if (vn || bn) return vn && (!bn || i < at);
+    return (MAX ? v > best : v < best) || (v == best && i < at);
+}
+template <bool MAX> ANVIL_HD static inline bool anvil_arg_better(int v, int i, int best, int at) {
+    return (MAX ? v > best : v < best) || (v == best && i < at);
+}
+// Partial picks over consecutive chunks of a whole-tensor reduction (no output index), combined as
+// the interpreter combines them (interp.py:484-516): a later chunk replaces the pick only if its
+// extreme (np.max / np.min: nan when the chunk holds one) is strictly better, so a nan in the
+// first chunk stays and a later chunk holding a nan is passed over.
+template <bool MAX> ANVIL_HD static inline bool anvil_chunk_better(float part, float acc) {
+    return MAX ? part > acc : part < acc;
+}
+template <bool MAX> ANVIL_HD static inline bool anvil_chunk_better(int part, int acc) {
+    return MAX ? part > acc : part < acc;
+}
 // sign keeps 0, -0 and nan as they are (np.sign).
 ANVIL_HD static inline float anvil_signf(float a) { return a > 0.0f ? 1.0f : (a < 0.0f ? -1.0f : a); }
 ANVIL_HD static inline int anvil_signi(int a) { return (0 < a) - (a < 0); }

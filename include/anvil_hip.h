@@ -37,7 +37,8 @@ int anvil_entry_device(void);
 
 /* One call of the lowered function that allocates nothing: no hipMalloc or hipFree, no pinned host
  * memory, no events or graphs. No counterpart in the reference; it is for callers that cannot
- * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * allocate (tight serving loops, harnesses that forbid it). It waits for `stream` before it
+ * returns, so it cannot itself be recorded while that stream is being captured into a graph.
  * inputs[k] / outputs[k] are the device buffers of argument k and result k (input_bytes[k] /
  * output_bytes[k] must equal their compiled sizes: shapes are fixed when a function is lowered);
  * the work is queued on `stream` (a hipStream_t; NULL: the null stream) and the call returns after

@@ -546,6 +546,71 @@ print(b)
 print(m)
 """
 
+# argmax / argmin as np.argmax / np.argmin decide (interp.py:478-481): the first of equal extremes,
+# a nan before every number (the first nan), rows of -inf and of zeros; one lane per row (20), a
+# wavefront per row (64), a workgroup per row (256, 5000, 8192), whole tensors, and whole tensors
+# past the interpreter's chunk of 2^22 elements, whose chunk picks meet by its own rule (a later
+# chunk holding a nan is passed over: gA's 9.0 never wins)
+ARGPICK = """
+const BIG = 4198400
+neg: [2] = -1.0
+bad = sqrt(neg)
+zero: [2] = 0.0
+ninf = log(zero)
+s20[i, j] = f32((j * 7 + i) % 5) where i < 300, j < 20
+n20[i, j] = (bad[0] if (j == i % 23 and i % 3 == 0) else (ninf[0] if i % 7 == 1 else s20[i, j]))
+a20[i] = argmax n20[i, j]
+b20[i] = argmin n20[i, j]
+print(a20)
+print(b20)
+t64[i, j] = f32((j * 5 + i * 3) % 8) where i < 256, j < 64
+n64[i, j] = (bad[0] if j == (i * 13) % 80 else (ninf[0] if i % 11 == 5 else t64[i, j]))
+a64[i] = argmax n64[i, j]
+b64[i] = argmin n64[i, j]
+print(a64)
+print(b64)
+t256[i, j] = f32((j * 37 + i) % 61) where i < 6, j < 256
+n256[i, j] = (bad[0] if (i == 2 and j == 200) or (i == 4 and (j == 3 or j == 250)) else t256[i, j])
+rz[i, j] = max(t256[i, j] - 100.0, 0.0)
+a256[i] = argmax n256[i, j]
+b256[i] = argmin n256[i, j]
+c256[i] = argmax rz[i, j]
+d256[i] = argmin rz[i, j]
+print(a256)
+print(b256)
+print(c256)
+print(d256)
+t5k[i, j] = f32((j * 13 + i * 7) % 97) where i < 3, j < 5000
+n5k[i, j] = (bad[0] if i == 1 and j == 4700 else t5k[i, j])
+a5k[i] = argmax n5k[i, j]
+b5k[i] = argmin n5k[i, j]
+print(a5k)
+print(b5k)
+t8k[i, j] = f32((j * 29 + i) % 101) where i < 2, j < 8192
+n8k[i, j] = (bad[0] if i == 0 and (j == 8000 or j == 8191) else t8k[i, j])
+a8k[i] = argmax n8k[i, j]
+b8k[i] = argmin n8k[i, j]
+print(a8k)
+print(b8k)
+w[j] = f32((j * 7919) % 1000) where j < 300000
+wn[j] = (bad[0] if j == 250001 else w[j])
+print(argmax(w))
+print(argmin(w))
+print(argmax(wn))
+print(argmin(wn))
+g[j] = f32(j % 5) where j < BIG
+gA[j] = (bad[0] if j == 4194400 else (9.0 if j == 4194500 else g[j]))
+gB[j] = (bad[0] if j == 3000000 or j == 10 else g[j])
+gC[j] = (9.0 if j == 4194310 else g[j])
+gD[j] = (-3.0 if j == 4194305 or j == 17 else g[j])
+print(argmax(gA))
+print(argmin(gA))
+print(argmax(gB))
+print(argmax(gC))
+print(argmin(gD))
+"""
+
+C4_MID = {"STEPS": 2, "BATCH": 4, "T": 32, "D": 64, "HEADS": 2, "LAYERS": 1}
 C1_KEEP = ["net.l1.W", "net.l1.b", "net.l2.W", "net.l2.b", "perm"]
 C2_KEEP = ["net.l1.W", "net.l1.b", "net.l2.W", "net.l2.b", "net.l3.W", "net.l3.b", "perm"]
 
@@ -685,5 +750,31 @@ S: [7, 300] = 0.0
 S[tok[n, t], d] += X[n, t, d] * 2.0 - 1.0
 print(G[0:2])
 print(S[5:7])
+"""},
+    {"name": "argpick", "source": ARGPICK, "interp": True, "own_process": True},
+    # attention chains the fused training attention must leave to the generated kernels (IR only):
+    # queries and keys read from the same columns of qkv (their gradients add into one slice), and
+    # a projection with a fourth slice that no head reads (its gradient is 0, written by no launch);
+    # the generated kernels then run against the reference interpreter's vectors
+    {"name": "attn_same_qk", "own_process": True, "interp": True, "keep": ["net.layers.0.Wqkv"],
+     "source": C4.replace("qkv[n, u, 1, h, c]", "qkv[n, u, 0, h, c]"), "consts": C4_MID},
+    {"name": "attn_four_slices", "own_process": True, "interp": True, "keep": ["net.layers.0.Wqkv"],
+     "source": C4.replace("[D, 3 * D]", "[D, 4 * D]").replace("reshape(-1, T, 3, HEADS, DH)",
+                                                               "reshape(-1, T, 4, HEADS, DH)"),
+     "consts": C4_MID},
+    # a row block (one workgroup per row) whose second stage adds into rows that a kernel before the
+    # chain wrote (y, 256 elements a row): the stage must read the prior writer's values
+    {"name": "rowblock_prior", "interp": True, "own_process": True, "source": """
+X: [256, 256] ~ normal(0, 1)
+fn f(x: [n, m]):
+    y = x * 2.0
+    s[i] = sum y[i, j]
+    y[i, j] -= s[i] / 256.0
+    t[i, q] = sum y[i, 4 * q + c] where c < 4
+    return t
+for step in range(2):
+    r = f(X)
+    print(r[0:2, 0:3])
+    print(sum(r))
 """},
 ]

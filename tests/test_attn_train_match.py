@@ -139,3 +139,34 @@ def test_costs_count_the_causal_tile_pairs(name):
             assert hip_cost.plan_cost(p)[0] == want[p.kind]
             seen += 1
     assert seen == (12 if T > 160 else 8)
+
+
+@pytest.mark.parametrize("name", ["attn_same_qk", "attn_four_slices"])
+def test_slices_that_do_not_tile_the_gradient_keep_the_chain(name):
+    """The fused backward stores dQ, dK and dV at the Q, K and V slices of G in place of `G = 0` and
+    three `+=`: only right when the slices cover G once each. Queries and keys read from the same
+    columns (attn_same_qk: their gradients must add) and a projection with a fourth, unread slice
+    (attn_four_slices: its gradient must be 0) keep the generated kernels, forward and backward;
+    tests/test_hip_gpu.py runs both against the reference interpreter's vectors."""
+    prog, data = load_ir(name)
+    g, src = _gen(prog, data)
+    assert not any(p.kind.startswith("attention-train") for p in g.plans)
+    assert "anvil_attn_fwd" not in src
+
+
+def test_slice_cover_rule():
+    """_slices_tile on hand-made layouts: C4's [n, t, 3, h, c] (q0, k0, v0 = 0, H·D, 2·H·D)
+    tiles; two slices at one offset, a gap, a slice past the end and an overlap by one do not."""
+    from anvil.backend.hip_attn_train import _Shape, _slices_tile
+    sh = _Shape()
+    sh.B, sh.H, sh.T, sh.D = 2, 2, 4, 8
+    HD = sh.H * sh.D
+    sh.qh, sh.qs = sh.D, 3 * HD
+    sh.qn = sh.T * sh.qs
+    n = sh.B * sh.qn
+    for (q0, k0, v0), ok in (((0, HD, 2 * HD), True), ((2 * HD, 0, HD), True), ((0, 0, 2 * HD), False),
+                             ((0, HD, HD), False), ((0, HD, 2 * HD + 1), False), ((0, HD - 1, 2 * HD), False)):
+        sh.q0, sh.k0, sh.v0 = q0, k0, v0
+        assert _slices_tile(sh, n) is ok, (q0, k0, v0)
+    sh.q0, sh.k0, sh.v0 = 0, HD, 2 * HD
+    assert not _slices_tile(sh, n + 1)           # one element of G no slice covers

@@ -17,11 +17,11 @@ from hiprun import check_program_run, function_call, kept_buffers, outputs_match
 PROGRAMS = ["greet", "logreg", "attention_fit", "split", "scatter", "integers", "formats", "control",
             "products", "c1_small", "c2_small", "c2_steps100", "mnist_like", "c4_small", "c4_mid", "c5_small", "c5_mid",
             "files", "picks", "ckpt_write", "ckpt_read", "serial", "draws", "board", "c5_conv12", "c4_t160",
-            "scatter_rows"]
+            "scatter_rows", "argpick", "attn_same_qk", "attn_four_slices", "rowblock_prior"]
 FUNCTIONS = ["c3_softmax_small", "c3_layernorm_small", "c3_linear_small", "c3_linear_tall", "c3_attention_small",
              "c3_attention_d64", "c3_attention_d128"]
 TRAINED = {"c2_steps100", "c2_small", "c1_small", "mnist_like", "logreg", "attention_fit", "c5_mid", "c4_mid",
-           "c5_conv12", "c4_t160"}
+           "c5_conv12", "c4_t160", "attn_same_qk", "attn_four_slices"}
 
 
 @pytest.mark.parametrize("name", PROGRAMS)

@@ -55,3 +55,27 @@ def test_rowblock_lanes_follow_the_row_count():
     assert _rowblock_lanes(_source("c4_t256_2")) == {(4096, 128)}
     assert _rowblock_lanes(_source("c2_wide_mlp")) == {(256, 256)}
     assert {lanes for _, lanes in _rowblock_lanes(_source("c4_full2"))} == {256}      # 1024 rows
+
+
+def _rowblock_plan(prog, data):
+    g = hip.HipGen(prog, seed=data.get("seed", 0))
+    g.generate()
+    (p,) = [p for p in g.plans if p.kind == "rowblock"]
+    return p
+
+
+def test_rowblock_keeps_no_lds_shadow_of_a_buffer_read_before_the_chain_writes_it():
+    """rowblock_prior: y = 2x (before the chain), then the chain s = Σ y, y -= s / 256, t = Σ y[..4].
+    The `+=` stage reads y's values from the kernel ahead of the launch, so y must stay in memory
+    only: an LDS copy of the row would start empty. Also with y taken as a temporary that only the
+    chain reads (which alone would make its row slice live in LDS, and its memory store dropped)."""
+    prog, data = load_ir("rowblock_prior")
+    p = _rowblock_plan(prog, data)
+    y = [b for b in prog.buffers if b.name == "y" and b.kind == "var"][0]
+    assert y.id in p.before_ids and y.id not in p.shadow
+    prog, data = load_ir("rowblock_prior")
+    y = [b for b in prog.buffers if b.name == "y" and b.kind == "var"][0]
+    y.kind = "temp"
+    p = _rowblock_plan(prog, data)
+    assert len(p.kernels) == 3 and y.id not in p.shadow and y.id not in p.dead
+    assert f"sh{y.id}" not in p.source()
