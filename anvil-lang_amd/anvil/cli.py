@@ -2,7 +2,7 @@
 
     python -m anvil hip   PROG.json [-o PROG.hip] [--seed N]     write the generated .hip file
     python -m anvil build PROG.json [-o PROG.so]  [--seed N]     compile it for gfx950
-    python -m anvil run   PROG.json [--seed N] [--profile] [--check[=inf]] [--dump OUT.npz --keep a,b,...]
+    python -m anvil run   PROG.json [--seed N] [--profile | --profile-rates] [--check[=inf]] [--dump OUT.npz --keep a,...]
     python -m anvil export FN.json [-o DIR] [--name LIB]        a function as lib<LIB>.so + <LIB>.h
 
 These mirror the reference's `anvil cuda file.anvil` and `anvil run|build --cuda` (cli.py:259-270,
@@ -49,7 +49,10 @@ def main(argv=None) -> int:
         if name in ("hip", "build"):
             q.add_argument("-o", "--output", default=None)
         if name == "run":
-            q.add_argument("--profile", action="store_true", help="per-kernel device time, on stderr")
+            q.add_argument("--profile", action="store_true",
+                           help="time every launch and print the reference's breakdown at exit (stdout)")
+            q.add_argument("--profile-rates", action="store_true",
+                           help="time every launch; per launch ms, share, calls, GFLOP/s and GB/s on stderr")
             q.add_argument("--dump", default=None, help="write the final contents of --keep buffers here (.npz)")
             q.add_argument("--keep", default="", help="comma-separated buffer names (or #id) to dump")
             q.add_argument("--marks", default=None, help="record an event per iteration of loops with this counter")
@@ -78,14 +81,17 @@ def main(argv=None) -> int:
         hip.build(src, out, emulate=args.emulate)
         return 0
     lib = hip.HipLibrary(hip.compile_source(src, emulate=args.emulate), src)
-    if args.profile:
+    profiling = args.cmd == "run" and (args.profile or args.profile_rates)
+    if profiling:
         lib.lib.anvil_profile_enable(1)
     if args.marks:
         lib.lib.anvil_marks_select(args.marks.encode())
     sys.stdout.flush()
     rc = lib.main()
     lib.lib.anvil_sync_device()
-    if args.profile:
+    if args.cmd == "run" and args.profile:
+        lib.lib.anvil_profile_print()           # the reference prints its table when the program ends
+    if args.cmd == "run" and args.profile_rates:
         rows = sorted(lib.profile(), key=lambda r: -r[1])
         total = sum(r[1] for r in rows) or 1.0
         sys.stderr.write(f"{'ms':>10} {'%':>6} {'calls':>8} {'GFLOP/s':>9} {'GB/s':>8}  kernel\n")

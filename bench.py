@@ -221,9 +221,25 @@ def c3_run(calls: int) -> dict:
                             "achieved": round(ach, 2), "unit": "TFLOP/s" if mfma else "GB/s",
                             "frac": round(ach / peak, 4), "flops": flops, "bytes": nbytes})
         fn.lib.lib.anvil_profile_enable(0)
-        out[name] = {"us_per_call_kernels": round(sum(k["mean_us"] for k in kernels), 2), "kernels": kernels}
+        out[name] = {"us_per_call_kernels": round(sum(k["mean_us"] for k in kernels), 2), "kernels": kernels,
+                     "library": os.path.basename(fn.lib.path)}
     return {"metric": "C3 anvil.function kernels vs roofline (device-resident inputs)", "calls": calls,
             "functions": out}
+
+
+C3_CALLS = 20
+
+
+def c3_summary(run: dict) -> dict:
+    """Per C3 function: its library, kernel time per call and every kernel's mean time and roofline
+    fraction (the bench line's compact form of c3_run)."""
+    out = {"calls": run["calls"], "timing": "HIP events around each launch on the library's stream, "
+                                            "inputs resident in device memory"}
+    for name, f in run["functions"].items():
+        out[name] = {"library": f["library"], "us_per_call_kernels": f["us_per_call_kernels"],
+                     "kernels": [{k: r[k] for k in ("kernel", "mean_us", "bound", "achieved", "unit", "frac")}
+                                 for r in f["kernels"]]}
+    return out
 
 
 def host_description() -> str:
@@ -388,7 +404,8 @@ def main() -> int:
     p.add_argument("--profile-table", action="store_true", help="print every kernel's time to stderr")
     p.add_argument("--graphs", action="store_true", help="replay loop bodies as HIP graphs")
     p.add_argument("--copy", action="store_true", help="run the copy kernel that calibrates HBM counters")
-    p.add_argument("--c3", action="store_true", help="config C3: the standalone functions, per kernel")
+    p.add_argument("--c3", action="store_true", help="config C3 alone: the standalone functions, per kernel")
+    p.add_argument("--no-c3", action="store_true", help="skip config C3's functions in the default line")
     p.add_argument("--yardstick", nargs="?", const="c2", choices=sorted(YARDSTICK_SHAPES),
                    help="torch.mm (the vendor library) on a config's product shapes (default c2)")
     p.add_argument("--oracle-leg", nargs=3, metavar=("IR", "COUNTER", "STOP"), help=argparse.SUPPRESS)
@@ -446,6 +463,8 @@ def main() -> int:
         line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
     if not args.no_c1:
         line["c1_epoch"] = c1_epoch(cpu=not args.no_cpu)
+    if not args.no_c3:
+        line["c3"] = c3_summary(c3_run(C3_CALLS))
     print(json.dumps(line), flush=True)
     return 0
 

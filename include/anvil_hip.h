@@ -75,6 +75,8 @@ double anvil_profile_ms(int site);        /* total device time */
 long anvil_profile_calls(int site);
 double anvil_profile_flops(int site);     /* algorithmic FLOPs of one launch (cost.py:22-37 rules) */
 double anvil_profile_bytes(int site);     /* algorithmic bytes of one launch (cost.py:40-52 rules) */
+const char *anvil_profile_where(int site); /* the row text of the --profile table: name, label, file:line */
+void anvil_profile_print(void);          /* the --profile table on stdout (runtime.s:1592-1671 form) */
 
 /* ---- loop marks: a device event at the start of each iteration of the loops whose counter has
  * this name, for timing exactly K iterations. No counterpart in the reference. ---------------- */

@@ -30,9 +30,10 @@ NUMBER = re.compile(r"[-+]?(?:\d+\.\d*|\.\d+|\d+)(?:[eE][-+]?\d+)?|[-+]?inf|nan"
 
 
 def run_program(name_or_path: str, emulate: bool, keep=(), timeout: int = 600, cwd=None, env_extra=None,
-                check=None, stdin: str = "", out_dir=None):
+                check=None, stdin: str = "", out_dir=None, extra_args=()):
     """(exit status, stdout, stderr, {buffer name: final contents}). stdin: what `input` reads;
-    out_dir: where the files the program writes go ($ANVIL_OUT; the library is the same build)."""
+    out_dir: where the files the program writes go ($ANVIL_OUT; the library is the same build);
+    extra_args: more options of `anvil run` (--profile)."""
     path = name_or_path if name_or_path.endswith(".json") else ir_path(name_or_path)
     with tempfile.TemporaryDirectory() as d:
         dump = os.path.join(d, "out.npz")
@@ -43,6 +44,7 @@ def run_program(name_or_path: str, emulate: bool, keep=(), timeout: int = 600, c
             cmd.append(f"--check={check}")
         if keep:
             cmd += ["--dump", dump, "--keep", ",".join(keep)]
+        cmd += list(extra_args)
         env = dict(os.environ, PYTHONPATH=ROOT_PKG + os.pathsep + os.environ.get("PYTHONPATH", ""))
         env.update(env_extra or {})
         if out_dir is not None:
