@@ -10,7 +10,8 @@ One row per launch of the generated program, in program order: its share of the 
 total milliseconds and number of launches, then the launch's name (6 columns), what it computes
 (the labels of the IR kernels it runs, joined by '+', 34 columns) and the source line of its first
 kernel. The launch counts are held to the NumPy oracle's count of executions of the same IR
-kernels, the labels and lines to the IR the reference front end wrote.
+kernels (summed over the launches that hold a kernel), the labels and lines to the IR the
+reference front end wrote.
 """
 import io
 import os
@@ -57,8 +58,17 @@ def oracle_launch_counts(name: str) -> dict:
     return counts
 
 
+# launches that finish another's work (partial sums added, the second half of a backward, the device
+# twins of host scalars): they run the same IR kernels again and are not counted as executions
+SECOND = {"gemm-reduce", "slices-sum", "attention-train-dkdv", "twin"}
+
+
+def _second(p) -> bool:
+    return p.kind in SECOND or (p.kind == "fused" and all(_second(q) for q in p.parts))
+
+
 def expected_rows(name: str, emulate: bool):
-    """(name, label, loc, first IR kernel id) of each launch, in program order."""
+    """(name, label, loc, IR kernel ids or None for a second launch) of each launch, in program order."""
     from anvil.backend import hip
     prog, data = load_ir(name)
     g = hip.HipGen(prog, seed=int(data.get("seed", 0)), emulate=emulate)
@@ -68,7 +78,7 @@ def expected_rows(name: str, emulate: bool):
         row = hip.profile_row(p)
         nm = row.split(" ", 1)[0]
         rest = row[max(6, len(nm)) + 1:]
-        out.append((nm, rest[:34], rest[35:], p.kernels[0].id))
+        out.append((nm, rest[:34], rest[35:], None if _second(p) else [k.id for k in p.kernels]))
     return out
 
 
@@ -80,12 +90,17 @@ def check_table(name: str, emulate: bool):
     assert program == plain                                   # the program's own output is unchanged
     want = expected_rows(name, emulate)
     assert [r[3] for r in rows] == [w[0] for w in want]       # every launch, in program order
+    # every IR kernel runs in the launches that hold it (a fused launch, or on the iteration that
+    # leaves the loop the part of it before the exit) as often as the oracle executes it
     counts = oracle_launch_counts(name)
-    prog, data = load_ir(name)
-    for (pct, ms, calls, nm, label, loc), (wn, wlabel, wloc, kid) in zip(rows, want):
+    ran: dict = {}
+    for (pct, ms, calls, nm, label, loc), (wn, wlabel, wloc, kids) in zip(rows, want):
         assert (label, loc) == (wlabel, wloc), nm
-        assert calls == counts.get(kid, 0), (nm, calls, counts.get(kid, 0))
         assert ms >= 0 and 0 <= pct <= 100
+        for kid in kids or []:
+            ran[kid] = ran.get(kid, 0) + calls
+    assert ran and all(ran[k] == counts.get(k, 0) for k in ran), \
+        {k: (ran[k], counts.get(k, 0)) for k in ran if ran[k] != counts.get(k, 0)}
     assert abs(sum(r[1] for r in rows) - total) <= 0.05 * len(rows) + 0.1
     if total > 0:
         assert abs(sum(r[0] for r in rows) - 100) <= 0.05 * len(rows) + 0.1
@@ -103,7 +118,7 @@ def test_profile_table_form_cpu_build():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["c2_small", "c4_mid"])
+@pytest.mark.parametrize("name", ["c2_small", "c4_mid", "c5_mid"])
 def test_profile_table_on_the_gpu(name):
     """The same table from the gfx950 build: the launches (fused side-by-side and row-block launches
     included) in program order, each counted as often as the oracle executes its IR kernels, and
