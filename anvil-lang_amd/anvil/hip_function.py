@@ -44,20 +44,23 @@ class Lowered:
         by_id = {b.id: b for b in prog.buffers}
         fn = data["function"]
         outs = [None if i is None else by_id[i] for i in fn["outputs"]]
-        return Lowered(prog, [by_id[i] for i in fn["inputs"]], outs, name=fn.get("name", "fn"),
-                       tuple_result=len(outs) > 1)
+        return Lowered(prog, [by_id[i] for i in fn["inputs"]], outs, consts=fn.get("consts", ()),
+                       name=fn.get("name", "fn"), tuple_result=fn.get("tuple_result", len(outs) > 1))
 
 
 class Compiled:
-    def __init__(self, name, lowered: Lowered, seed: int = 0):
+    """emulate: the generated file built as plain C++ for the CPU (a test build, never a fallback;
+    call_device then has no device to use)."""
+
+    def __init__(self, name, lowered: Lowered, seed: int = 0, emulate: bool = False):
         self.name = name
         self.prog = lowered.prog
         self.inputs = lowered.inputs
         self.outputs = lowered.outputs
         self.consts = lowered.consts
         self.tuple_result = lowered.tuple_result
-        self.source = hip.generate(self.prog, seed=seed, library=True)
-        self.lib = hip.HipLibrary(hip.compile_source(self.source), self.source)
+        self.source = hip.generate(self.prog, seed=seed, library=True, emulate=emulate)
+        self.lib = hip.HipLibrary(hip.compile_source(self.source, emulate=emulate), self.source)
         exported = set()
         for b in self.inputs + [o for o in self.outputs if o is not None]:
             try:

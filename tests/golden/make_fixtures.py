@@ -100,13 +100,17 @@ def main(ref_root: str) -> None:
         os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
         if spec.get("function"):
             fn = spec["function"]
-            sig = tuple(("tensor", tuple(shape), dtype) for shape, dtype in fn["args"])
+            # a tensor argument is (shape, dtype); a Python number passed to the function is
+            # ("const", its Anvil text), a compile-time constant (pyapi.arguments)
+            sig = tuple(("const", a[1]) if a[0] == "const" else ("tensor", tuple(a[0]), a[1]) for a in fn["args"])
             low = pyapi.lower(spec["source"], path, fn["name"], sig, seed=spec.get("seed", 0))
             prog = low.prog
             data = irjson.dump(prog)
             data["function"] = {"name": fn["name"], "inputs": [b.id for b in low.inputs],
                                 "outputs": [None if b is None else b.id for b in low.outputs],
-                                "arg_names": list(low.arg_names), "out_names": list(low.out_names)}
+                                "arg_names": list(low.arg_names), "out_names": list(low.out_names),
+                                "consts": [c.item() if hasattr(c, "item") else c for c in low.consts],
+                                "tuple_result": bool(low.tuple_result)}
         else:
             prog = compile_text(spec["source"], path=path, consts=spec.get("consts"),
                                 optimize=spec.get("optimize", True)).program
@@ -140,7 +144,8 @@ def main(ref_root: str) -> None:
         arrays = {}
         if spec.get("function"):
             rng = np.random.default_rng(spec["function"].get("input_seed", 2))
-            for k, (b, (shape, dtype)) in enumerate(zip(low.inputs, spec["function"]["args"])):
+            tensor_args = [a for a in spec["function"]["args"] if a[0] != "const"]
+            for k, (b, (shape, dtype)) in enumerate(zip(low.inputs, tensor_args)):
                 x = (rng.standard_normal(shape).astype(np.float32) if dtype == "f32"
                      else rng.integers(0, spec["function"].get("int_hi", 10), shape).astype(np.int32))
                 it.arr(b)[:b.numel] = x.reshape(-1)

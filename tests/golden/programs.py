@@ -777,4 +777,41 @@ for step in range(2):
     print(r[0:2, 0:3])
     print(sum(r))
 """},
+    # C4 and C5 over their whole BASELINE runs (200 Adam steps at T = 64; 300 SGD steps), the loss
+    # printed every 20 (30) steps along the way and the trained weights kept
+    {"name": "c4_full200", "own_process": True, "interp": True,
+     "source": C4.replace('    if step == 0:\n        print("step 1 loss {loss:.6e}")',
+                          '    if step == 0 or step % 20 == 19:\n        print("step {step + 1} loss {loss:.6e}")'),
+     "keep": ["net.layers.0.Wqkv", "net.layers.3.ff_in.W", "net.head.W", "net.head.b"]},
+    {"name": "c5_full300", "own_process": True, "interp": True,
+     "source": C5.replace('    if step == 0:\n        print("step 1 loss {loss:.6e}")',
+                          '    if step == 0 or step % 30 == 29:\n        print("step {step + 1} loss {loss:.6e}")'),
+     "keep": ["net.c1.W", "net.c1.b", "net.c2.W", "net.c2.b", "net.fc1.W", "net.fc2.W"]},
+] + [
+    # anvil.function's surface as the reference's tests/test_pyapi.py:32-134 uses it, one lowering
+    # (pyapi.lower) per argument signature: an i32 argument and a number passed as a compile-time
+    # constant (two versions), a constant used as a shape, a loss-and-gradient tuple with a scalar,
+    # a scalar result, a compile-time result beside a tensor one, a function that assigns into its
+    # argument, a float64 / transposed argument, a NumPy scalar argument (threads call it), causal
+    # attention
+    {"name": f"fn_{name}", "source": src, "interp": True, "own_process": True, "function": {"name": fname, "args": args}}
+    for name, src, fname, args in [
+        ("pick", "fn pick(x: [n, d], idx: i32[k], scale) = x[idx] * scale\n", "pick",
+         [([10, 3], "f32"), ([3], "i32"), ("const", "2.0")]),
+        ("pick_half", "fn pick(x: [n, d], idx: i32[k], scale) = x[idx] * scale\n", "pick",
+         [([10, 3], "f32"), ([2], "i32"), ("const", "0.5")]),
+        ("shifted", "fn shifted(x: [n], k):\n    y[i] = x[i + k] where i < n - k\n    return y\n", "shifted",
+         [([6], "f32"), ("const", "2")]),
+        ("loss_grad", "fn loss_and_grad(w: [d], x: [n, d], y: [n]):\n    loss = mean((x @ w - y) ** 2)\n"
+                      "    return loss, grad(loss, w)\n", "loss_and_grad", [([5], "f32"), ([32, 5], "f32"), ([32], "f32")]),
+        ("total", "fn total(x) = sum(x)\n", "total", [([10], "f32")]),
+        ("sizes", "fn sizes(x: [n, d]):\n    return n * d, sum(x)\n", "sizes", [([3, 4], "f32")]),
+        ("keeps_args", "fn f(x: [n]):\n    x[0] = 1.0\n    return x * 2\n", "f", [([4], "f32")]),
+        ("double", "fn double(x) = x * 2\n", "double", [([4, 3], "f32")]),
+        # a NumPy scalar argument arrives as a [1] tensor (pyapi.arguments: np.ascontiguousarray)
+        ("scaled", "fn scaled(x, s) = x * s\n", "scaled", [([1000], "f32"), ([1], "f32")]),
+        ("causal", "fn attention(q: [b, t, d], k: [b, t, d], v: [b, t, d]):\n"
+                   "    s[n, i, j] = sum q[n, i, c] * k[n, j, c] / sqrt(d) + (0.0 if j <= i else -1e9)\n"
+                   "    return softmax(s) @ v\n", "attention", [([3, 7, 4], "f32")] * 3),
+    ]
 ]
