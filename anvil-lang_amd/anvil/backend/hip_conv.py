@@ -392,7 +392,40 @@ def match_dgrad(gen, stmts: list, i: int):
         return None
     plan = DgradPlan(gen, [G] + ([zero] if zero is not None else []) + [S], f"k{G.id}", G, S, zero is not None,
                      s.alpha, ops, rows, korder, side_pred, tvars, sst, M, N, K)
-    return plan, j + 1 - i
+    used = j + 1 - i
+    covered = zero is not None or (ir.prod(t[1] for t in targets) == dX.numel and not sst.offset.const)
+    if (covered and i + used < len(stmts) and isinstance(stmts[i + used], KernelStmt)
+            and os.environ.get("ANVIL_HIP_MAP_FUSE", "1") != "0"):
+        fwd = dgrad_follower(gen, plan, stmts[i + used].kernel, dX)
+        if fwd is not None:
+            plan.follow(stmts[i + used].kernel, fwd)
+            used += 1
+    return plan, used
+
+
+def dgrad_follower(gen, plan, e: ir.Kernel, dX):
+    """The loads of dX of elementwise kernel e, if e can run in the input gradient's epilogue
+    element by element (ReLU's gradient after a convolution's: dZ = dX·(z > 0)): e walks dX's
+    elements in row-major order, reads dX only at its own element, and neither writes what the
+    product reads or writes nor reads anything else it writes; else None."""
+    if (e.red is not None or e.uses_rand() or A.is_host_kernel(e, gen.hosts) or not A.parallel_safe(e)
+            or any(st.accumulate for st in e.stores) or ir.prod(v.extent for v in e.domain) != dX.numel):
+        return None
+    lin = ir.Affine(0)
+    for v, st in zip(e.domain, ir.row_major_strides([v.extent for v in e.domain])):
+        lin = lin + ir.Affine(0, {v: st})
+    fwd = []
+    for ld in A.kernel_loads(e):
+        if ld.buf.root is dX:
+            if ld.offset != lin:
+                return None
+            fwd.append(ld)
+    if not fwd:
+        return None
+    product_io = {b.id for k in plan.kernels for b in A.kernel_reads(k)} | {dX.id}
+    if {b.id for b in A.kernel_writes(e)} & product_io:
+        return None
+    return fwd
 
 
 class DgradPlan(Plan):
@@ -422,6 +455,35 @@ class DgradPlan(Plan):
         self.tm, self.tn = -(-M // (32 * TM)), -(-N // (32 * TN))
         nch = -(-(K // 8) // W)
         self.nch, self.depth = nch, min(2 if nch <= 32 else 4, nch)
+        self.follower, self.fwd, self.dx_dead = None, [], False
+
+    def follow(self, e, fwd):
+        """Run elementwise kernel e (which reads dX only at its own element) on each dX element as
+        it is computed; dX itself is then not stored unless something else reads it."""
+        dX = self.sst.buf.root
+        self.follower, self.fwd = e, fwd
+        self.kernels.append(e)
+        self.label += " + " + (e.label or e.name)
+        inside = sum(1 for k in self.kernels if dX.id in {b.id for b in A.kernel_reads(k)})
+        self.dx_dead = (dX.kind in A.SHARED_KINDS and not self.gen.is_host(dX) and not getattr(dX, "heap", False)
+                        and self.gen.readers.get(dX.id, 0) == inside)
+
+    def hoistable(self):
+        """The follower's plain loads of buffers it does not write, other than dX (at most two)."""
+        if self.follower is None:
+            return []
+        e, out, seen = self.follower, [], set()
+        fwd = {id(ld) for ld in self.fwd}
+        written = {b.id for b in A.kernel_writes(e)}
+        for ld in A.kernel_loads(e):
+            if (id(ld) in fwd or ld.buf.root.id in written or not ld.buf.root.shape or ld.offset.gathers()
+                    or ld.offset.scalars()):
+                continue
+            key = (ld.buf.root.id, ld.offset.key() if hasattr(ld.offset, "key") else repr(ld.offset))
+            if key not in seen:
+                seen.add(key)
+                out.append(ld)
+        return out[:2]
 
     def grid(self):
         return (self.tn, self.tm, 1), 64 * self.W
@@ -458,26 +520,66 @@ class DgradPlan(Plan):
         a_ks, b_ks = self.ops[0][3].coef(inner), self.ops[1][3].coef(inner)
         chk = lambda x, t: "true" if x % t else "false"
         per = 16 // W
-        body += [f"    float part[{TM}][{TN}][{per}];",
-                 f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, ANVIL_LD_ANY, ANVIL_LD_ANY, {self.nch}, {self.depth}, "
-                 f"{chk(self.M, 32 * TM)}, {chk(self.N, 32 * TN)}>(part, pa, arow, ak, {a_ks}LL, pb, brow, bk, "
-                 f"{b_ks}LL, {self.M}, {self.N}, m0, n0, 0, {self.K}, opa, opb, apred, bpred);",
-                 "    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;",
-                 "#pragma unroll",
-                 f"    for (int ijq = 0; ijq < {TM * TN * per}; ijq++) {{",
-                 f"        const int ti = ijq / {TN * per}, tj = (ijq / {per}) % {TN}, q = ijq % {per};",
-                 f"        const int vv = {per} * wave + q;",
-                 "        const int mi = m0 + 32 * ti + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
-                 "        const int ni = n0 + 32 * tj + (lane & 31);",
-                 f"        if (mi >= {self.M} || ni >= {self.N}) continue;"]
+        # the follower's other loads (ReLU's z at the element) are issued before the product
+        elem = ["#pragma unroll",
+                f"    for (int ijq = 0; ijq < {TM * TN * per}; ijq++) {{",
+                f"        const int ti = ijq / {TN * per}, tj = (ijq / {per}) % {TN}, q = ijq % {per};",
+                f"        const int vv = {per} * wave + q;",
+                "        const int mi = m0 + 32 * ti + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);",
+                "        const int ni = n0 + 32 * tj + (lane & 31);",
+                f"        if (mi >= {self.M} || ni >= {self.N}) continue;"]
         dm, dn = _digits(self.rows[0], "mi"), _digits(self.rows[1], "ni")
         out = [str(self.sst.offset.const)] if self.sst.offset.const else []
         for tv, c in self.tvars:
             d = dm.get(tv, dn.get(tv))
             out.append(f"{c}LL * (long long){d}")
+        hoisted = self.hoistable()
+        if hoisted:
+            from .hip_kernels import decode
+            from .hip_emit import Emitter
+            e = self.follower
+            body.append("    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;")
+            body.append("    " + " ".join(f"float pre{h}[{TM * TN * per}];" for h in range(len(hoisted))))
+            body += elem
+            body.append(f"        const uint32_t lin_ = (uint32_t)({' + '.join(out) or '0'});")
+            pl: list[str] = []
+            pem = Emitter(sc, pl, "        ", prefix="p")
+            for line in decode(e.domain, "lin_", "uint32_t"):
+                pem.emit(line)
+            for h, ld in enumerate(hoisted):
+                pem.emit(f"pre{h}[ijq] = {pem.build(ld)};")
+            body += pl + ["    }"]
+        body += [f"    float part[{TM}][{TN}][{per}];",
+                 f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, ANVIL_LD_ANY, ANVIL_LD_ANY, {self.nch}, {self.depth}, "
+                 f"{chk(self.M, 32 * TM)}, {chk(self.N, 32 * TN)}>(part, pa, arow, ak, {a_ks}LL, pb, brow, bk, "
+                 f"{b_ks}LL, {self.M}, {self.N}, m0, n0, 0, {self.K}, opa, opb, apred, bpred);"]
+        if not hoisted:
+            body.append("    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;")
+        body += elem
         target = f"{sc.buf(self.sst.buf)}[{' + '.join(out)}]"
         base = "0.0f" if self.zeroed else target
-        body.append(f"        {target} = {base} + {flit(self.alpha)} * part[ti][tj][q];")
+        if self.follower is None:
+            body.append(f"        {target} = {base} + {flit(self.alpha)} * part[ti][tj][q];")
+        else:
+            from .hip_kernels import canon_key, decode
+            from .hip_emit import Emitter
+            e = self.follower
+            body.append(f"        const float dx_ = {base} + {flit(self.alpha)} * part[ti][tj][q];")
+            if not self.dx_dead:
+                body.append(f"        {target} = dx_;")
+            body.append(f"        const uint32_t lin_ = (uint32_t)({' + '.join(out) or '0'});")
+            lines: list[str] = []
+            em = Emitter(sc, lines, "        ")
+            for line in decode(e.domain, "lin_", "uint32_t"):
+                em.emit(line)
+            canon = {v: ("e", v.id) for v in e.domain}
+            sc.canon = canon
+            sc.fwd = {canon_key(ld.buf, ld.offset, canon): "dx_" for ld in self.fwd}
+            for h, ld in enumerate(hoisted):
+                sc.fwd[canon_key(ld.buf, ld.offset, canon)] = f"pre{h}[ijq]"
+            self.statements(em, e, sc, parallel=True)
+            sc.canon, sc.fwd = None, {}
+            body += lines
         body.append("    }")
         head = [f"// conv-dgrad: {self.G.name} (product into an im2col-shaped gradient) and {self.S.name} (its "
                 f"scatter) as one product · {self.M}x{self.N}x{self.K}, window terms over the edge skipped",

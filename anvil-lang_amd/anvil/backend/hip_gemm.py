@@ -458,10 +458,11 @@ def follower_map(k: ir.Kernel, e: ir.Kernel):
     return m
 
 
-def follower(k: ir.Kernel, e: ir.Kernel, hosts: set):
-    """(var map, forwarded loads) if elementwise kernel e can run in k's epilogue, element by element:
-    every load e makes of what k writes is of the element k just wrote there (so the value comes
-    from a register), and k reads nothing that e writes."""
+def follower(k: ir.Kernel, e: ir.Kernel, hosts: set, prior=()):
+    """(var map, forwarded loads) if elementwise kernel e can run in k's epilogue, element by element,
+    after the followers already taken (prior: (kernel, its var map) pairs): every load e makes of
+    what k or a prior follower writes is of the element written there in the same lane (a value of
+    k's comes from a register), and neither k nor a prior follower reads anything that e writes."""
     if (e.red is not None or e.uses_rand() or A.is_host_kernel(e, hosts) or not A.parallel_safe(e)
             or any(st.accumulate for st in e.stores)):
         return None
@@ -474,17 +475,26 @@ def follower(k: ir.Kernel, e: ir.Kernel, hosts: set):
             return None
         stored[st.buf.root.id] = st.offset
     added = {st.buf.root.id for st in k.stores if st.accumulate}   # k adds to them: no value to forward
+    later = {}                          # buffers prior followers store to: the element, in k's variables
+    for f, mf in prior:
+        for st in f.stores:
+            off = subst_affine(st.offset, mf)
+            if off is None or later.get(st.buf.root.id, off) != off:
+                return None
+            later[st.buf.root.id] = off
     fwd = []
     for ld in A.kernel_loads(e):
         bid = ld.buf.root.id
         if bid in added:
             return None
-        if bid in stored:
+        if bid in stored or bid in later:
             sub = subst_affine(ld.offset, m)
-            if sub is None or sub != stored[bid]:
+            if sub is None or sub != later.get(bid, stored.get(bid)):
                 return None
-            fwd.append(ld)
-    if {b.id for b in A.kernel_writes(e)} & {b.id for b in A.kernel_reads(k)}:
+            if bid not in later:
+                fwd.append(ld)
+    readers = {b.id for f in [k] + [f for f, _ in prior] for b in A.kernel_reads(f)}
+    if {b.id for b in A.kernel_writes(e)} & readers:
         return None
     return m, fwd
 

@@ -182,6 +182,20 @@ class KernelScope(Scope):
         return got
 
 
+def _subst(off: ir.Affine, m: dict):
+    """off with each loop variable replaced by its affine function in m (None if off has a gather
+    or a variable m does not map)."""
+    out = ir.Affine(off.const)
+    for t, c in off.terms.items():
+        if isinstance(t, Var) and t in m:
+            out = out + m[t] * c
+        elif isinstance(t, ScalarRef):
+            out = out + ir.Affine(0, {t: c})
+        else:
+            return None
+    return out
+
+
 def canon_key(buf, off: ir.Affine, canon: dict):
     terms = []
     for t, c in off.terms.items():
@@ -314,6 +328,11 @@ class Plan:
 # ----------------------------------------------------------------------------- map
 
 class MapPlan(Plan):
+    """One lane per element of the domain (grid-stride), with the elementwise kernels that follow it
+    over the same elements (each reads what this one just stored at that element: the gradient of
+    a max-pool, then ReLU's) run in the same lane on the value in a register; a store that only
+    those followers read is dropped."""
+
     kind = "map"
 
     def __init__(self, gen, k, name):
@@ -321,12 +340,35 @@ class MapPlan(Plan):
         self.k = k
         self.total = ir.prod(v.extent for v in k.domain)
         self.threads = THREADS
+        self.followers = []             # (kernel, var map, forwarded loads), run per element after k
+        self.vector_width()
+
+    def vector_width(self):
         # four consecutive elements per lane and step when every access is unit-stride along the
         # innermost variable: the compiler merges them into 16-byte loads and stores
+        k = self.k
         inner = k.domain[-1] if k.domain else None
-        self.V = 4 if (inner is not None and not gen.emulate and inner.extent % 4 == 0
-                       and unit_stride(k, inner)) else 1
+        unit = inner is not None and unit_stride(k, inner)
+        for e, m, _ in self.followers:
+            for off in [ld.offset for ld in A.kernel_loads(e)] + [st.offset for st in e.stores]:
+                sub = _subst(off, m)
+                unit = unit and sub is not None and sub.coef(inner) in (0, 1)
+        self.V = 4 if (unit and not self.gen.emulate and inner.extent % 4 == 0) else 1
         self.blocks = max(1, min(-(-self.total // (THREADS * self.V)), MAX_BLOCKS))
+
+    def absorb(self, e, how):
+        """Take elementwise kernel e as a follower (how: its var map and forwarded loads, from
+        hip_gemm.follower), unless it writes a buffer this plan writes (two lanes' elements could
+        then land on one element in either order)."""
+        m, fwd = how
+        written = {b.id for p in [self.k] + [f[0] for f in self.followers] for b in A.kernel_writes(p)}
+        if {b.id for b in A.kernel_writes(e)} & written:
+            return False
+        self.followers.append((e, m, fwd))
+        self.kernels.append(e)
+        self.label += " + " + (e.label or e.name)
+        self.vector_width()
+        return True
 
     def source(self) -> str:
         k = self.k
@@ -338,7 +380,21 @@ class MapPlan(Plan):
         em = Emitter(sc, body, ind)
         for line in decode(k.domain, "u", it):
             em.emit(line)
-        self.statements(em, k, sc, parallel=True)
+        stored = {}
+
+        def on_store(st, val):
+            if not st.accumulate:
+                stored[st.buf.root.id] = val
+        self.statements(em, k, sc, parallel=True, on_store=on_store)
+        for e, m, fwd in self.followers:
+            em.reset_memo()
+            for ev, aff in m.items():
+                em.emit(f"const int v{ev.id} = (int)({em.affine(aff)});")
+            canon = {v: ("e", v.id) for v in e.domain}
+            sc.canon = canon
+            sc.fwd = {canon_key(ld.buf, ld.offset, canon): stored[ld.buf.root.id] for ld in fwd}
+            self.statements(em, e, sc, parallel=True, on_store=on_store)
+            sc.canon, sc.fwd = None, {}
         n = self.total // self.V
         head = [self.comment() + (f" · {self.V} elements per lane" if self.V > 1 else ""), self.header(self.threads),
                 f"    for ({it} w = ({it})blockIdx.x * {self.threads}u + threadIdx.x; w < {n}u; "
