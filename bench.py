@@ -312,6 +312,64 @@ def cpu_baseline(steps: int):
                       f"at run time, threadpoolctl); host: {run['host']}; {t:.1f} s"}
 
 
+# configs C4 (character transformer at T = 256, 200 Adam steps) and C5 (the CNN, 300 SGD steps):
+# their own step loops at full size, reported beside the metric
+STEP_CONFIGS = {
+    "c4": ("c4_transformer_t256.json", 200, "C4: decoder-only char transformer, B 16, T 256, D 256, 4 heads, "
+           "4 layers, MLP 4D, causal attention, layernorm, vocab 96, adam, 200-step program"),
+    "c5": ("c5_cnn.json", 300, "C5: CNN conv3x3 1->32 + ReLU, conv3x3 32->64 + ReLU, 2x2 maxpool, 9216->128->10, "
+           "cross_entropy, sgd(0.05), batch 128, 300-step program"),
+}
+
+
+def config_steps(name: str, warmup: int = 10) -> dict:
+    """One of STEP_CONFIGS: ms per step over its step loop after `warmup` steps (device events at
+    the loop marks of the timed region's two ends), then a profiled run for the serial roofline of
+    the step (each launch at its own bound, summed) and the launch with the most device time."""
+    from anvil import irjson
+    from anvil.backend import hip
+    fname, steps, workload = STEP_CONFIGS[name]
+    with open(os.path.join(ROOT, "tests", "golden", "ir", fname)) as f:
+        data = json.load(f)
+    lib = hip.load(irjson.load(data), seed=int(data.get("seed", 0)))
+    lib.lib.anvil_marks_select(b"step")
+    lib.lib.anvil_marks_window(warmup, steps - 1)
+    with quiet_stdout():
+        rc = lib.main()
+        lib.lib.anvil_sync_device()
+    if rc != 0:
+        raise SystemExit(f"bench: {name} exited with status {rc}")
+    ms = lib.lib.anvil_marks_elapsed_ms(warmup, steps - 1)
+    if ms < 0:
+        raise SystemExit(f"bench: {name} marked {lib.lib.anvil_marks_count()} steps, fewer than {steps}")
+    ms /= steps - 1 - warmup
+    lib.lib.anvil_marks_select(b"")
+    lib.lib.anvil_profile_enable(1)
+    lib.lib.anvil_profile_reset()
+    with quiet_stdout():
+        lib.main()
+        lib.lib.anvil_sync_device()
+    prof = lib.profile()
+    lib.lib.anvil_profile_enable(0)
+    t_roof, top = 0.0, None
+    for label, tms, calls, flops, nbytes in prof:
+        if calls >= steps:
+            t_roof += calls / steps * max(flops / PEAK_FP32_MFMA, nbytes / PEAK_HBM)
+            if top is None or tms > top[1]:
+                top = (label, tms, calls, flops, nbytes)
+    label, tms, calls, flops, nbytes = top
+    t = tms / calls * 1e-3
+    mfma = flops / max(nbytes, 1) > PEAK_FP32_MFMA / PEAK_HBM
+    achieved = flops / t / 1e12 if mfma else nbytes / t / 1e9
+    peak = PEAK_FP32_MFMA / 1e12 if mfma else PEAK_HBM / 1e9
+    return {"workload": workload, "ms_per_step": round(ms, 5), "steps_timed": steps - 1 - warmup,
+            "timing": "HIP events at the step loop's marks, no profiling", "library": os.path.basename(lib.path),
+            "step_roofline": {"t_roofline_us": round(t_roof * 1e6, 2), "frac": round(t_roof * 1e3 / ms, 4)},
+            "dominant_launch": {"kernel": label, "mean_us": round(t * 1e6, 3), "bound": "mfma" if mfma else "hbm",
+                                "achieved": round(achieved, 1 if not mfma else 3),
+                                "unit": "TFLOP/s" if mfma else "GB/s", "frac": round(achieved / peak, 4)}}
+
+
 C1_WORKLOAD = os.path.join(ROOT, "tests", "golden", "ir", "c1_mlp.json")
 C1_BATCH = 64
 
@@ -406,6 +464,7 @@ def main() -> int:
     p.add_argument("--copy", action="store_true", help="run the copy kernel that calibrates HBM counters")
     p.add_argument("--c3", action="store_true", help="config C3 alone: the standalone functions, per kernel")
     p.add_argument("--no-c3", action="store_true", help="skip config C3's functions in the default line")
+    p.add_argument("--no-c45", action="store_true", help="skip configs C4 and C5's step loops in the default line")
     p.add_argument("--yardstick", nargs="?", const="c2", choices=sorted(YARDSTICK_SHAPES),
                    help="torch.mm (the vendor library) on a config's product shapes (default c2)")
     p.add_argument("--oracle-leg", nargs=3, metavar=("IR", "COUNTER", "STOP"), help=argparse.SUPPRESS)
@@ -465,6 +524,9 @@ def main() -> int:
         line["c1_epoch"] = c1_epoch(cpu=not args.no_cpu)
     if not args.no_c3:
         line["c3"] = c3_summary(c3_run(C3_CALLS))
+    if not args.no_c45:
+        for name in STEP_CONFIGS:
+            line[name] = config_steps(name)
     print(json.dumps(line), flush=True)
     return 0
 
