@@ -393,7 +393,8 @@ def match_dgrad(gen, stmts: list, i: int):
     plan = DgradPlan(gen, [G] + ([zero] if zero is not None else []) + [S], f"k{G.id}", G, S, zero is not None,
                      s.alpha, ops, rows, korder, side_pred, tvars, sst, M, N, K)
     used = j + 1 - i
-    covered = zero is not None or (ir.prod(t[1] for t in targets) == dX.numel and not sst.offset.const)
+    # every element of dX is computed here (so the follower meets each one), at its row-major index
+    covered = ((zero is not None or ir.prod(t[1] for t in targets) == dX.numel) and not sst.offset.const)
     if (covered and i + used < len(stmts) and isinstance(stmts[i + used], KernelStmt)
             and os.environ.get("ANVIL_HIP_MAP_FUSE", "1") != "0"):
         fwd = dgrad_follower(gen, plan, stmts[i + used].kernel, dX)
