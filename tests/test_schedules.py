@@ -79,3 +79,22 @@ def test_rowblock_keeps_no_lds_shadow_of_a_buffer_read_before_the_chain_writes_i
     p = _rowblock_plan(prog, data)
     assert len(p.kernels) == 3 and y.id not in p.shadow and y.id not in p.dead
     assert f"sh{y.id}" not in p.source()
+
+
+def test_row_chain_stops_before_a_real_product():
+    """C4's loss head, log-softmax -> the cross-entropy gradient -> the softmax gradient over 4096
+    rows of 96, is one row block that ends where dlogits·W (K = 96, a matrix-core product) begins;
+    without the cut the whole chain was refused and ran as four launches (measured on the step
+    loop: T = 64 548 -> 541 us, T = 256 1415 -> 1406 us per step)."""
+    src = _source("c4_transformer_t256")
+    head = [l for l in src.splitlines() if l.startswith("// rowblock: ") and "reduce max j<96" in l]
+    assert len(head) == 1 and "x k<256]" not in head[0], head           # the product is not a stage
+    assert re.search(r"^// gemm: .*· 4096x256x96 · ", src, re.M)
+    import os
+    os.environ["ANVIL_HIP_ROWBLOCK_CUT"] = "0"
+    try:
+        uncut = _source("c4_transformer_t256")
+    finally:
+        del os.environ["ANVIL_HIP_ROWBLOCK_CUT"]
+    assert not any(l.startswith("// rowblock: ") and "reduce max j<96" in l for l in uncut.splitlines())
+    assert uncut.count("__global__") == src.count("__global__") + 3
