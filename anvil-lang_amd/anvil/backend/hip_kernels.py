@@ -1885,6 +1885,12 @@ class FusedPlan(Plan):
         # parts that finish in a second launch (partial tiles or slices, then their sum): those
         # second launches follow this one, side by side in turn
         self.kslices = max(getattr(p, "kslices", 1) for p in parts)
+        self.joined_reads: set = set()      # what a second launch that joined this one reads
+
+    def extra_reads(self) -> set:
+        """Buffers read beyond the IR kernels of the parts: those of an earlier plan whose second
+        launch runs here."""
+        return set(self.joined_reads)
 
     def second(self):
         seconds = [p.second() for p in self.parts if getattr(p, "kslices", 1) > 1]

@@ -9,6 +9,7 @@ import re
 
 from fixtures import load_ir
 
+from anvil import ir
 from anvil.backend import hip
 
 
@@ -98,3 +99,68 @@ def test_row_chain_stops_before_a_real_product():
         del os.environ["ANVIL_HIP_ROWBLOCK_CUT"]
     assert not any(l.startswith("// rowblock: ") and "reduce max j<96" in l for l in uncut.splitlines())
     assert uncut.count("__global__") == src.count("__global__") + 3
+
+
+def _split_product_then_nine(dependent):
+    """C = Aᵀ·B (64 x 64 outputs, K = 8192: few tiles and a long K, so K is split across workgroups
+    and a second launch adds the partial tiles), then eight independent maps; with `dependent`, a
+    ninth kernel reads C transposed (not at its own element, so it is no epilogue of the product)."""
+    M = N = 64
+    K = 8192
+    A = ir.Buffer("A", (K, M), "f32", "data")
+    B = ir.Buffer("B", (K, N), "f32", "data")
+    C = ir.Buffer("C", (M, N), "f32", "var")
+    m, n, k = ir.Var("m", M), ir.Var("n", N), ir.Var("k", K)
+    g = ir.Kernel([m, n], [ir.Store(C, ir.Affine(0, {m: N, n: 1}), ir.Acc())],
+                  red=ir.Reduction([k], "sum", ir.Binary("mul", ir.Load(A, ir.Affine(0, {k: M, m: 1})),
+                                                          ir.Load(B, ir.Affine(0, {k: N, n: 1})))), name="g")
+    body, bufs = [ir.KernelStmt(g)], [A, B, C]
+    for j in range(8):
+        L = 1000 + 8 * j                                    # extents apart: no map is another's follower
+        x, y = ir.Buffer(f"x{j}", (L,), "f32", "data"), ir.Buffer(f"y{j}", (L,), "f32", "var")
+        i = ir.Var("i", L)
+        body.append(ir.KernelStmt(ir.Kernel([i], [ir.Store(y, ir.Affine(0, {i: 1}),
+                                                            ir.Unary("exp", ir.Load(x, ir.Affine(0, {i: 1}))))],
+                                            name=f"e{j}")))
+        bufs += [x, y]
+    if dependent:
+        a, b = ir.Var("a", M), ir.Var("b", N)
+        yc = ir.Buffer("yc", (M, N), "f32", "var")
+        body.append(ir.KernelStmt(ir.Kernel([a, b], [ir.Store(yc, ir.Affine(0, {a: N, b: 1}),
+                                                               ir.Unary("exp", ir.Load(C, ir.Affine(0, {b: N, a: 1}))))],
+                                            name="t")))
+        bufs.append(yc)
+    body += [ir.Print([ir.PrintItem("tensor", buf=x)]) for x in bufs if x.kind == "var"]
+    return ir.Program(ir.Block(body), bufs)
+
+
+def _launch_labels(src):
+    return [l.split("// ", 1)[1] for l in src.split("static int anvil_program", 1)[1].splitlines()
+            if re.match(r"\s*\{   // ", l) and "on the host" not in l]
+
+
+def test_a_second_launch_joins_the_next_independent_launch():
+    """The partial-tile sum of a K split runs side by side with the next launch when no data passes
+    between them: the first launch holds the product and seven maps (eight parts at most), the
+    eighth map then shares the sum's launch. A kernel that reads the product keeps the sum alone."""
+    labels = _launch_labels(hip.generate(_split_product_then_nine(False)))
+    assert labels[0].startswith("k") and labels[0].count(" map: ") == 7 and " gemm: g" in labels[0]
+    assert " map: e7 | " in labels[1] and "gemm-reduce: partial-tile sum + g" in labels[1], labels
+    labels = _launch_labels(hip.generate(_split_product_then_nine(True)))
+    assert labels[1] == "partial-tile sum + g", labels
+    assert "map: e7" in labels[2] and "map: t" in labels[2]
+
+
+def test_c4_and_c5_weight_update_sums_join_the_next_launch(monkeypatch):
+    """C5: the loss kernel (one workgroup) runs beside the four weight updates' sums; C4 at T = 256:
+    three of the four partial-tile sums run beside the next weight-gradient launch (the last one has
+    no launch after it in the step). Measured on the step loops: C5 211.5 -> 209.3 us, C4 1405 ->
+    1399 us per step."""
+    c5 = _launch_labels(_source("c5_cnn"))
+    assert any(l.startswith("k") and "rows: cross_entropy" in l and "gemm-reduce" in l for l in c5), c5
+    c4 = _launch_labels(_source("c4_transformer_t256"))
+    alone = [l for l in c4 if "partial-tile sum" in l and " gemm: " not in l]
+    assert len(alone) == 1, alone
+    monkeypatch.setenv("ANVIL_HIP_JOIN", "0")
+    assert len(_launch_labels(_source("c5_cnn"))) == len(c5) + 1
+    assert len(_launch_labels(_source("c4_transformer_t256"))) == len(c4) + 3
