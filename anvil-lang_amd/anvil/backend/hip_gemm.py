@@ -726,11 +726,12 @@ class GemmPlan(Plan):
         products) takes the XCD-aware order: in launch order, linear id mod 8 would be the tile
         column whenever the columns are a multiple of 8, so every XCD would read all of A (3-5 µs
         of 35 measured). Square grids measured faster in launch order (C2's weight gradients)."""
-        if (os.environ.get("ANVIL_GEMM_SWIZZLE", "1") == "0" or self.tn * self.tm < 16
-                or self.tm < 8 * self.tn):
+        mode = os.environ.get("ANVIL_GEMM_SWIZZLE", "1")
+        if mode == "0" or self.tn * self.tm < 16 or (self.tm < 8 * self.tn and mode != "all"):
             return f"    const int m0 = blockIdx.y * {self.BM}, n0 = blockIdx.x * {self.BN};"
+        G = int(os.environ.get("ANVIL_GEMM_SWIZZLE_ROWS", "8"))
         return (f"    int tx_, ty_;\n"
-                f"    anvil_tile_of(blockIdx.y * {self.tn} + blockIdx.x, {self.tn}, {self.tm}, 8, tx_, ty_);\n"
+                f"    anvil_tile_of(blockIdx.y * {self.tn} + blockIdx.x, {self.tn}, {self.tm}, {G}, tx_, ty_);\n"
                 f"    const int m0 = ty_ * {self.BM}, n0 = tx_ * {self.BN};")
 
     def k_table(self, which) -> str:
