@@ -721,11 +721,40 @@ class GemmPlan(Plan):
         sc.fwd, sc.canon = saved
         return "\n".join([f"    auto {name} = [=](float x) -> float {{"] + lines + [f"        return {v};", "    };"])
 
-    def tile_origin(self) -> str:
-        """m0, n0 of the workgroup's tile. A tall grid (tile rows ≥ 8 × tile columns: C4's 4096 x 256
+    def run_order(self):
+        """Which grids give each XCD one contiguous run of tiles (anvil_run_of) instead of every
+        eighth: "split", a K split across workgroups, its runs walking slice by slice, so the tiles
+        that read one slice's K range of both operands share an L2 (C5's update launch fetched
+        250 MB against 89 MB of algorithmic reads in launch order, 83 MB in runs: 58.8 -> 52.3 µs;
+        C4's weight gradients measured the same either way). With $ANVIL_GEMM_RUNS=all also
+        "wide", a grid of 8 or more tile columns per row (C5's forward convolution: adjacent
+        position tiles read overlapping input rows), its runs walking the tile rows of one column
+        before the next: the convolution's fetch 64.9 -> 11.7 MB at the same 39 µs, and the step no
+        faster, so it is not the default. None for the others."""
+        mode = os.environ.get("ANVIL_GEMM_RUNS", "1")
+        if mode == "0":
+            return None
+        if self.kslices > 1:
+            return "split"
+        if (mode == "all" and self.s.B == 1 and self.tn >= 8 * self.tm and self.tn * self.tm >= 16):
+            return "wide"
+        return None
+
+    def tile_origin(self, runs=None) -> str:
+        """m0, n0 of the workgroup's tile (and, for a K split in runs, zr_: its slice and batch
+        index). A tall grid (tile rows ≥ 8 × tile columns: C4's 4096 x 256
         products) takes the XCD-aware order: in launch order, linear id mod 8 would be the tile
         column whenever the columns are a multiple of 8, so every XCD would read all of A (3-5 µs
         of 35 measured). Square grids measured faster in launch order (C2's weight gradients)."""
+        tiles = self.tn * self.tm
+        if runs == "split":
+            return (f"    const int p_ = anvil_run_of(((int)blockIdx.z * {self.tm} + (int)blockIdx.y) * {self.tn} "
+                    f"+ (int)blockIdx.x, {tiles * self.s.B * self.kslices});\n"
+                    f"    const uint32_t zr_ = (uint32_t)(p_ / {tiles});\n"
+                    f"    const int m0 = (p_ % {tiles}) / {self.tn} * {self.BM}, n0 = (p_ % {tiles}) % {self.tn} * {self.BN};")
+        if runs == "wide":
+            return (f"    const int p_ = anvil_run_of((int)blockIdx.y * {self.tn} + (int)blockIdx.x, {tiles});\n"
+                    f"    const int m0 = (p_ % {self.tm}) * {self.BM}, n0 = (p_ / {self.tm}) * {self.BN};")
         mode = os.environ.get("ANVIL_GEMM_SWIZZLE", "1")
         if mode == "0" or self.tn * self.tm < 16 or (self.tm < 8 * self.tn and mode != "all"):
             return f"    const int m0 = blockIdx.y * {self.BM}, n0 = blockIdx.x * {self.BN};"
@@ -838,14 +867,15 @@ class GemmPlan(Plan):
         a_ptr = sc.buf(s.la.buf)
         b_ptr = sc.buf(s.lb.buf)
         body = [self.operand(sc, s.ea, s.la, "opa"), self.operand(sc, s.eb, s.lb, "opb"),
-                self.tile_origin(),
+                self.tile_origin(self.run_order()),
                 "    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;"]
         ca, cb = s.la.offset.coef, s.lb.offset.coef
         a_off = [str(s.la.offset.const)]
         b_off = [str(s.lb.offset.const)]
         zsrc = "blockIdx.z"
         if self.kslices > 1:
-            body.append(f"    const uint32_t slice = blockIdx.z % {self.kslices}u, bz = blockIdx.z / {self.kslices}u;")
+            z = "zr_" if self.run_order() == "split" else "blockIdx.z"
+            body.append(f"    const uint32_t slice = {z} % {self.kslices}u, bz = {z} / {self.kslices}u;")
             zsrc = "bz"
         if s.batch:
             body += ["    " + line for line in decode(s.batch, zsrc, "uint32_t")]

@@ -39,6 +39,13 @@ typedef int anvil_i32x4 __attribute__((ext_vector_type(4)));
 // own L2: tile (tx, ty) of a tn x tm grid for linear id L is chosen so that the ids one XCD receives
 // (L mod 8 = x) cover one contiguous run p of tiles, and runs are walked in groups of G tile rows,
 // column by column: an XCD's tiles then share few row panels of A and column panels of B.
+__device__ __forceinline__ int anvil_run_of(int L, int n) {
+    // the position in 0 .. n - 1 of linear id L when the ids of XCD x = L mod 8 take one contiguous
+    // run of positions (runs of n / 8, the first n mod 8 of them one longer)
+    const int q = n / 8, rem = n % 8;
+    return (L % 8) * q + min(L % 8, rem) + L / 8;
+}
+
 __device__ __forceinline__ void anvil_tile_of(int L, int tn, int tm, int G, int &tx, int &ty) {
     const int n = tn * tm, q = n / 8, rem = n % 8;
     const int x = L % 8, r = L / 8;

@@ -5,6 +5,7 @@
 - `ANVIL_GEMM_FORCE=<schedule>@MxNxK` changes the products of that shape only;
 - row blocks of more than 2048 rows run with 128 lanes per row, shorter ones with 256.
 """
+import os
 import re
 
 from fixtures import load_ir
@@ -164,3 +165,46 @@ def test_c4_and_c5_weight_update_sums_join_the_next_launch(monkeypatch):
     monkeypatch.setenv("ANVIL_HIP_JOIN", "0")
     assert len(_launch_labels(_source("c5_cnn"))) == len(c5) + 1
     assert len(_launch_labels(_source("c4_transformer_t256"))) == len(c4) + 3
+
+
+def test_xcd_runs_are_one_contiguous_run_per_xcd(tmp_path):
+    """anvil_run_of (hip_rt/anvil_mfma.h), compiled for the host from the header's own text: for
+    every grid size up to 3000, the positions of ids 0 .. n - 1 are a permutation of 0 .. n - 1,
+    and the ids of each XCD (id mod 8) take one contiguous run of them."""
+    import subprocess
+    hdr = open(os.path.join(os.path.dirname(hip.__file__), "hip_rt", "anvil_mfma.h")).read()
+    start = hdr.index("__device__ __forceinline__ int anvil_run_of")
+    fn = hdr[start:hdr.index("\n}\n", start) + 3]
+    prog = ("#include <algorithm>\n#include <cstdio>\n#include <vector>\nusing std::min;\n"
+            "#define __device__\n#define __forceinline__ inline\n" + fn + r"""
+int main() {
+    for (int n = 1; n <= 3000; n++) {
+        std::vector<int> seen(n, 0), lo(8, n), hi(8, -1), cnt(8, 0);
+        for (int L = 0; L < n; L++) {
+            const int p = anvil_run_of(L, n);
+            if (p < 0 || p >= n || seen[p]++) { printf("n %d L %d p %d\n", n, L, p); return 1; }
+            lo[L % 8] = std::min(lo[L % 8], p); hi[L % 8] = std::max(hi[L % 8], p); cnt[L % 8]++;
+        }
+        for (int x = 0; x < 8; x++)
+            if (cnt[x] && hi[x] - lo[x] + 1 != cnt[x]) { printf("n %d xcd %d not contiguous\n", n, x); return 1; }
+    }
+    return 0;
+}
+""")
+    (tmp_path / "runs.cpp").write_text(prog)
+    subprocess.run(["g++", "-O1", "-o", str(tmp_path / "runs"), str(tmp_path / "runs.cpp")], check=True)
+    r = subprocess.run([str(tmp_path / "runs")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
+
+
+def test_split_products_walk_xcd_runs(monkeypatch):
+    """Every K split across workgroups takes its tile and slice from anvil_run_of (C5: the FC1
+    product and both convolutions' weight gradients); ANVIL_GEMM_RUNS=0 keeps launch order, and
+    =all adds the two wide grids (the second convolution, the FC1 input gradient)."""
+    src = _source("c5_cnn")
+    heads = re.findall(r"^// gemm: .*K in \d+ slices.*\n(?:.*\n){1,12}?.*anvil_run_of\(", src, re.M)
+    assert src.count("anvil_run_of(") == 1 + 3 and len(heads) == 3
+    monkeypatch.setenv("ANVIL_GEMM_RUNS", "0")
+    assert _source("c5_cnn").count("anvil_run_of(") == 1
+    monkeypatch.setenv("ANVIL_GEMM_RUNS", "all")
+    assert _source("c5_cnn").count("anvil_run_of(") == 1 + 3 + 2
