@@ -582,10 +582,10 @@ class GemmPlan(Plan):
         # the epilogue (see GemmReducePlan)
         tiles = -(-s.M // self.BM) * -(-s.N // self.BN) * s.B if self.pipe else -(-s.M // 32) * -(-s.N // 32) * s.B
         self.kslices, self.kslice = 1, s.K
-        if (self.pipe and tiles * self.waves < CU_WAVES // 2
+        if (self.pipe and tiles * self.waves < int(os.environ.get("ANVIL_GEMM_SPLITK_WAVES", str(CU_WAVES // 2)))
                 and s.K >= int(os.environ.get("ANVIL_GEMM_SPLITK_MINK", "4096"))
                 and os.environ.get("ANVIL_GEMM_SPLITK", "1") != "0"):
-            S = max(2, min(1024 // tiles, s.K // 512))
+            S = int(os.environ.get("ANVIL_GEMM_SPLITK_S", "0")) or max(2, min(1024 // tiles, s.K // 512))
             self.kslice = -(-(-(-s.K // S)) // 8) * 8
             self.kslices = -(-s.K // self.kslice)
         # chunks of 8·G k (anvil_mm_tile_kpipe): two 16-byte loads per lane of an operand contiguous
