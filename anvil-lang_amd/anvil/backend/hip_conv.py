@@ -454,8 +454,14 @@ class DgradPlan(Plan):
             W, TM, TN = 4, 1, 1
         self.W, self.TM, self.TN = W, TM, TN
         self.tm, self.tn = -(-M // (32 * TM)), -(-N // (32 * TN))
-        nch = -(-(K // 8) // W)
-        self.nch, self.depth = nch, min(2 if nch <= 32 else 4, nch)
+        # k in chunks of 8·kg per wavefront, `depth` chunks of loads in flight ($ANVIL_DGRAD_KG,
+        # $ANVIL_DGRAD_DEPTH)
+        kg = int(os.environ.get("ANVIL_DGRAD_KG", "1"))
+        if K % (8 * kg * W):
+            kg = 1
+        nch = -(-(K // (8 * kg)) // W)
+        depth = int(os.environ.get("ANVIL_DGRAD_DEPTH", "0")) or (2 if nch <= 32 else 4)
+        self.kg, self.nch, self.depth = kg, nch, min(depth, nch)
         self.follower, self.fwd, self.dx_dead = None, [], False
 
     def follow(self, e, fwd):
@@ -550,9 +556,10 @@ class DgradPlan(Plan):
             for h, ld in enumerate(hoisted):
                 pem.emit(f"pre{h}[ijq] = {pem.build(ld)};")
             body += pl + ["    }"]
-        body += [f"    float part[{TM}][{TN}][{per}];",
+        body += [f"    __shared__ float anvil_kp_lds[{W * TM * TN * 16 * 64}];",
+                 f"    float part[{TM}][{TN}][{per}];",
                  f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, ANVIL_LD_ANY, ANVIL_LD_ANY, {self.nch}, {self.depth}, "
-                 f"{chk(self.M, 32 * TM)}, {chk(self.N, 32 * TN)}>(part, pa, arow, ak, {a_ks}LL, pb, brow, bk, "
+                 f"{chk(self.M, 32 * TM)}, {chk(self.N, 32 * TN)}, {self.kg}>(anvil_kp_lds, part, pa, arow, ak, {a_ks}LL, pb, brow, bk, "
                  f"{b_ks}LL, {self.M}, {self.N}, m0, n0, 0, {self.K}, opa, opb, apred, bpred);"]
         if not hoisted:
             body.append("    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;")

@@ -673,6 +673,8 @@ class GemmPlan(Plan):
             return 4 * (2 * 2 * self.slab * 33 + 4 * 16 * 64)
         if self.sched == "tile":
             return 2 * 4 * 16 * ((self.BM + 4) + (self.BN + 4))
+        if self.pipe:
+            return 0                   # anvil_kp_lds, declared in the kernel's own text
         return self.waves * self.ptm * self.ptn * 16 * 64 * 4
 
     def absorb(self, e, how):
@@ -942,9 +944,10 @@ class GemmPlan(Plan):
                          "opa, opb")
                 G = self.kgroup
                 nch = -(-(self.kslice // (8 * G)) // W)
-                main = [f"    float part[{TM}][{TN}][{16 // W}];",
+                main = [f"    __shared__ float anvil_kp_lds[{W * TM * TN * 16 * 64}];",
+                        f"    float part[{TM}][{TN}][{16 // W}];",
                         f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
-                        f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}, {G}, {self.chains}>(part, {kargs});"]
+                        f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}, {G}, {self.chains}>(anvil_kp_lds, part, {kargs});"]
             else:
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]

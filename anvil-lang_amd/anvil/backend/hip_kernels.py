@@ -1848,6 +1848,60 @@ def lds_bytes(plan) -> int:
     return total + getattr(plan, "template_lds", lambda: 0)()
 
 
+KP_LDS = re.compile(r"__shared__ float anvil_kp_lds\[(\d+)\];")
+LDS_PER_CU = 160 * 1024
+
+
+def fused_target(parts):
+    """Workgroups per CU for a side-by-side launch of products, or None to keep each part's LDS its
+    own (the launch then holds the sum of the parts' arrays). A workgroup runs one part, so the
+    parts' partial-tile arrays can share one; the launch's LDS then sets how many workgroups a CU
+    holds, chosen by the longest K a workgroup of the launch sums. Measured on the weight-gradient
+    launches (step loops): K = 4096 (C4 at T = 256) with one workgroup per CU (the arrays apart)
+    1394 us per step, two 1390, three 1421, four 1455; K = 1320 (C5's convolution weight gradient)
+    three 201 us, four 197.4, five 199.6, eight 215.6; K = 1024 (C4 at T = 64) one to three 542 us,
+    four 537, five 527.5, six 526.8; K = 256 (C2) four 53.4 us (the arrays apart), seven 54.1.
+    A launch with fewer than two such arrays keeps its own. $ANVIL_HIP_FUSED_WGS=<n> sets the
+    target, 0 keeps the arrays apart."""
+    force = os.environ.get("ANVIL_HIP_FUSED_WGS")
+    if force is not None:
+        return int(force) or None
+    if sum(1 for p in parts if KP_LDS.search(p._source if hasattr(p, "_source") else p.source())) < 2:
+        return None                                     # nothing to share
+    kwg = max((getattr(p, "kslice", 0) for p in parts if p.kind == "gemm"), default=0)
+    if kwg >= 4096:
+        return 2
+    if kwg > 1024:
+        return 4
+    if kwg > 512:
+        return 6
+    return None
+
+
+def fused_lds(parts) -> int:
+    """LDS of parts side by side, as the budget for joining them counts it: the sum of their arrays
+    unless they share one at more than two workgroups per CU (C4 at T = 256, two per CU: 1390 us
+    per step with the launches the sum allows, 1397.5 with the longer ones the shared size
+    allows)."""
+    target = fused_target(parts)
+    if target is None or target <= 2:
+        return sum(lds_bytes(p) for p in parts)
+    kp = rest = 0
+    for p in parts:
+        total = lds_bytes(p)
+        m = KP_LDS.search(p._source)
+        own = 4 * int(m.group(1)) if m else 0
+        kp, rest = max(kp, own), rest + total - own
+    return max(kp + rest, lds_for(target))
+
+
+def lds_for(target: int) -> int:
+    """LDS bytes per workgroup that let a CU hold `target` workgroups and no more: the middle of the
+    range (160 KB / (target + 1), 160 KB / target]."""
+    lo, hi = LDS_PER_CU // (target + 1), LDS_PER_CU // target
+    return (lo + hi) // 2 // 256 * 256
+
+
 def barrier_free(plan) -> bool:
     src = plan._source if hasattr(plan, "_source") else plan.source()
     plan._source = src
@@ -1930,8 +1984,17 @@ class FusedPlan(Plan):
 
     def source(self) -> str:
         texts, calls = [], []
+        pool, rest = 0, 0
+        target = fused_target(self.parts)
         for j, p in enumerate(self.parts):
             src = p._source if hasattr(p, "_source") else p.source()
+            m = KP_LDS.search(src)
+            if target is not None:
+                rest += lds_bytes(p) - (4 * int(m.group(1)) if m else 0)
+            if m and target is not None:
+                # a workgroup runs one part: the parts' partial tiles share one LDS array
+                pool = max(pool, int(m.group(1)))
+                src = src.replace(m.group(0), f"float *const anvil_kp_lds = anvil_fl_{self.name};", 1)
             _, t = p.grid()
             head = f"__global__ void __launch_bounds__({t}) {p.name}("
             assert head in src, p.name
@@ -1952,6 +2015,11 @@ class FusedPlan(Plan):
         for p in self.parts:
             self.bufs.update(p.bufs)
             self.hosts.update(p.hosts)
+        if pool:
+            # sized for the launch's workgroups per CU (fused_target)
+            pool = max(pool, (lds_for(target) - rest) // 4)
+            texts.insert(0, f"__shared__ float anvil_fl_{self.name}[{pool}];   // the parts' partial tiles, "
+                            f"{target} workgroups per CU")
         head = [f"// fused: {', '.join(p.name for p in self.parts)} side by side",
                 f"__global__ void __launch_bounds__({self.threads}) {self.name}({self.params()}) {{",
                 "    uint32_t b = blockIdx.x;"]

@@ -410,13 +410,14 @@ __device__ __forceinline__ void anvil_mm_wave_kpipe(anvil_mm_acc<TM, TN> &acc,
 template <int W, int TM, int TN, int AMODE, int BMODE, int NCH, int D, bool CHKM, bool CHKN, int G = 1, int CH = 1,
           class AROW, class BROW, class AK, class BK, class OPA, class OPB, class APRED = anvil_all_pred,
           class BPRED = anvil_all_pred>
-__device__ __forceinline__ void anvil_mm_tile_kpipe(float (&out)[TM][TN][16 / W],
+__device__ __forceinline__ void anvil_mm_tile_kpipe(float *__restrict__ part, float (&out)[TM][TN][16 / W],
                                                     const float *__restrict__ a, AROW arow, AK ak, long long a_ks,
                                                     const float *__restrict__ b, BROW brow, BK bk, long long b_ks,
                                                     int M, int N, int m0, int n0, int kbeg, int K, OPA opa, OPB opb,
                                                     APRED apred = APRED(), BPRED bpred = BPRED()) {
+    // part: the caller's LDS for the wavefronts' partial tiles, W·TM·TN·16·64 floats (a side-by-side
+    // launch gives all its parts the same array: a workgroup runs one part)
     constexpr int PER = 16 / W;
-    __shared__ float part[W * TM * TN * 16 * 64];
     const int lane = threadIdx.x & 63, r = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);     // uniform: scalar branches
     const int c0 = kbeg / (8 * G) + w * NCH, n = min(NCH, max(0, (kbeg + K) / (8 * G) - c0));

@@ -208,3 +208,32 @@ def test_split_products_walk_xcd_runs(monkeypatch):
     assert _source("c5_cnn").count("anvil_run_of(") == 1
     monkeypatch.setenv("ANVIL_GEMM_RUNS", "all")
     assert _source("c5_cnn").count("anvil_run_of(") == 1 + 3 + 2
+
+
+def test_weight_gradient_launches_share_partial_tile_lds(monkeypatch):
+    """A side-by-side launch of products gives all parts one partial-tile array (a workgroup runs
+    one part), sized for the workgroups per CU its longest per-workgroup K measured best with:
+    C4 at T = 256 (K = 4096) two, C4 at T = 64 (K = 1024) six, C5 (K = 1320) four; C2's update
+    launch (K = 256) keeps each part's own array. Measured on the step loops: 1397 -> 1385 us,
+    541 -> 526 us, 201 -> 197 us."""
+    def targets(name):
+        src = _source(name)
+        pools = re.findall(r"^__shared__ float anvil_fl_(\w+)\[(\d+)\];   // the parts' partial tiles, (\d) "
+                           r"workgroups per CU", src, re.M)
+        for fname, words, _ in pools:              # every part of that launch points at the pool
+            body = src[src.index(f"anvil_fl_{fname}["):src.index(f"// fused: ", src.index(f"anvil_fl_{fname}["))]
+            assert "__shared__ float anvil_kp_lds" not in body
+            assert body.count(f"float *const anvil_kp_lds = anvil_fl_{fname};") >= 2
+        return {int(t) for _, _, t in pools}, [int(w) for _, w, _ in pools]
+    assert targets("c4_transformer_t256")[0] == {2}
+    assert targets("c4_transformer")[0] == {6}
+    t5, words = targets("c5_cnn")
+    assert t5 == {4} and all(36864 // 2 <= 4 * w <= 36864 for w in words)
+    assert targets("c2_wide_mlp")[0] == set()
+    # the LDS that lets a CU (160 KB) hold exactly n workgroups
+    from anvil.backend import hip_kernels as HK
+    for n in range(1, 9):
+        b = HK.lds_for(n)
+        assert 160 * 1024 // b == n
+    monkeypatch.setenv("ANVIL_HIP_FUSED_WGS", "0")
+    assert targets("c4_transformer_t256")[0] == set()
