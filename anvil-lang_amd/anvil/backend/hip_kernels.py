@@ -1860,7 +1860,8 @@ def fused_target(parts):
     launches (step loops): K = 4096 (C4 at T = 256) with one workgroup per CU (the arrays apart)
     1394 us per step, two 1390, three 1421, four 1455; K = 1320 (C5's convolution weight gradient)
     three 201 us, four 197.4, five 199.6, eight 215.6; K = 1024 (C4 at T = 64) one to three 542 us,
-    four 537, five 527.5, six 526.8; K = 256 (C2) four 53.4 us (the arrays apart), seven 54.1.
+    four 537, five 527.5, six 526.8; K = 256 (C2) four 53.2 us (the arrays apart), two 57.8, three
+    54.4, five 53.4, seven 54.1.
     A launch with fewer than two such arrays keeps its own. $ANVIL_HIP_FUSED_WGS=<n> sets the
     target, 0 keeps the arrays apart."""
     force = os.environ.get("ANVIL_HIP_FUSED_WGS")
