@@ -945,9 +945,16 @@ class GemmPlan(Plan):
                 G = self.kgroup
                 nch = -(-(self.kslice // (8 * G)) // W)
                 main = [f"    __shared__ float anvil_kp_lds[{W * TM * TN * 16 * 64}];",
-                        f"    float part[{TM}][{TN}][{16 // W}];",
-                        f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
-                        f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}, {G}, {self.chains}>(anvil_kp_lds, part, {kargs});"]
+                        f"    float part[{TM}][{TN}][{16 // W}];"]
+                if getattr(self, "rowpro", None) is not None:
+                    # A's rows computed here from the row chain's input (hip_rowpro)
+                    main += self.rowpro.source(self, sc, W, TM, G, nch, chk(s.M, self.BM))
+                    main.append(f"    anvil_mm_tile_kpipe_areg<{W}, {TM}, {TN}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
+                                f"{chk(s.N, self.BN)}, {G}, {self.chains}>(anvil_kp_lds, part, xa_, pb, brow, bk, "
+                                f"{b_ks}LL, {s.N}, n0, opb);")
+                else:
+                    main.append(f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, {self.amode}, {self.bmode}, {nch}, {min(self.depth, nch)}, "
+                                f"{chk(s.M, self.BM)}, {chk(s.N, self.BN)}, {G}, {self.chains}>(anvil_kp_lds, part, {kargs});")
             else:
                 main = [f"    float part[1][1][{per}];",
                         f"    anvil_mm_tile_ksplit<{W}, 1, 1, {self.amode}, {self.bmode}, {self.unroll}>(part, {args});"]

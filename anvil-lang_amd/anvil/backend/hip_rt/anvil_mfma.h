@@ -454,6 +454,143 @@ __device__ __forceinline__ void anvil_mm_tile_kpipe(float *__restrict__ part, fl
             }
 }
 
+// A product whose A rows are computed in the kernel from the rows of another matrix (a layer
+// norm's output, normalized from its input with row statistics) before the K split above runs on
+// them. K is one whole row, split over the W wavefronts in NCH chunks of 8G k each; lane (r, h) of
+// wavefront w holds, for tile row i, the k of the kpipe layout: x[i][(c·G + g)·4 + s] is element
+// k = 8G(w·NCH + c) + 4G·h + 4g + s of row m0 + 32i + r. The raw row elements are loaded
+// (anvil_rowpro_load), the generated code turns them into the A values in place (row sums through
+// anvil_rowpro_sum), and anvil_mm_tile_kpipe_areg runs the products with A from those registers
+// and only B loaded, D chunks in flight.
+template <int TM, int NCH, int G, bool CHKM>
+__device__ __forceinline__ void anvil_rowpro_load(float (&x)[TM][NCH * 4 * G], const float *__restrict__ p,
+                                                  long long rs, int m0, int M) {
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int row = m0 + 32 * i + r;
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const int k = 8 * G * (w * NCH + c) + 4 * G * h + 4 * g;
+                anvil_f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                if (!CHKM || row < M) v = *(const anvil_f32x4 *)(p + (long long)row * rs + k);
+                x[i][(c * G + g) * 4 + 0] = v.x;
+                x[i][(c * G + g) * 4 + 1] = v.y;
+                x[i][(c * G + g) * 4 + 2] = v.z;
+                x[i][(c * G + g) * 4 + 3] = v.w;
+            }
+    }
+}
+
+// The k index of element q of the lane's row registers (the layout above).
+template <int NCH, int G>
+__device__ __forceinline__ int anvil_rowpro_k(int q) {
+    const int lane = threadIdx.x & 63, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = q / (4 * G), g = (q / 4) % G, s = q % 4;
+    return 8 * G * (w * NCH + c) + 4 * G * h + 4 * g + s;
+}
+
+// Each lane's partial sums of its rows (p[i], the lane's terms of row m0 + 32i + r) become the whole
+// rows' sums: the two half-waves added, then the W wavefronts' partials in wavefront order.
+// lds: W·TM·32 floats.
+template <int W, int TM>
+__device__ __forceinline__ void anvil_rowpro_sum(float (&p)[TM], float *__restrict__ lds) {
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        p[i] += __shfl_xor(p[i], 32, 64);
+        if (h == 0) lds[(w * TM + i) * 32 + r] = p[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        float s = lds[i * 32 + r];
+#pragma unroll
+        for (int src = 1; src < W; src++) s += lds[(src * TM + i) * 32 + r];
+        p[i] = s;
+    }
+    __syncthreads();
+}
+
+template <int W, int TM, int TN, int BMODE, int NCH, int D, bool CHKN, int G, int CH, class BROW, class BK, class OPB>
+__device__ __forceinline__ void anvil_mm_tile_kpipe_areg(float *__restrict__ part, float (&out)[TM][TN][16 / W],
+                                                         const float (&xa)[TM][NCH * 4 * G],
+                                                         const float *__restrict__ b, BROW brow, BK bk, long long b_ks,
+                                                         int N, int n0, OPB opb) {
+    constexpr int PER = 16 / W;
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c0 = w * NCH;
+    long long bo[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) bo[j] = (!CHKN || n0 + 32 * j + r < N) ? brow(n0 + 32 * j + r) : 0;
+    anvil_mm_acc<TM, TN> acc, acc2;
+    acc.zero();
+    if (CH > 1) acc2.zero();
+    float bb[D][TN][4 * G];
+    anvil_all_pred bpred;
+#define ANVIL_KPA_LOAD(d, c)                                                                               \
+    _Pragma("unroll") for (int g = 0; g < G; g++) {                                                        \
+        const int k_ = 8 * G * (c0 + (c)) + 4 * G * h + 4 * g;                                            \
+        long long kb_[4];                                                                                  \
+        anvil_koffs<BMODE>(bk, k_, b_ks, kb_);                                                             \
+        _Pragma("unroll") for (int j = 0; j < TN; j++)                                                     \
+            anvil_chunk_load_k<BMODE, CHKN>(*reinterpret_cast<float(*)[4]>(&bb[d][j][4 * g]), b, bo[j], kb_, \
+                                            n0 + 32 * j + r, N, bpred(n0 + 32 * j + r, k_));               \
+    }
+#pragma unroll
+    for (int c = 0; c < D; c++) ANVIL_KPA_LOAD(c, c)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+#pragma unroll
+        for (int s = 0; s < 4 * G; s++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    if (CH > 1 && (s & 1))
+                        acc2.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[i][c * 4 * G + s], opb(bb[c % D][j][s]),
+                                                                            acc2.c[i][j], 0, 0, 0);
+                    else
+                        acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[i][c * 4 * G + s], opb(bb[c % D][j][s]),
+                                                                           acc.c[i][j], 0, 0, 0);
+                }
+        if (c + D < NCH) ANVIL_KPA_LOAD(c % D, c + D)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#undef ANVIL_KPA_LOAD
+    if (CH > 1) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc.c[i][j] += acc2.c[i][j];
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) part[(((w * TM + i) * TN + j) * 16 + v) * 64 + lane] = acc.c[i][j][v];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int q = 0; q < PER; q++) {
+                float s = 0.f;
+#pragma unroll
+                for (int src = 0; src < W; src++) s += part[(((src * TM + i) * TN + j) * 16 + PER * w + q) * 64 + lane];
+                out[i][j][q] = s;
+            }
+}
+
 // The K split with operands staged through LDS: the workgroup's 256 lanes load each KC-deep chunk
 // of A (32 rows) and B (32 columns) with 16-byte loads along whichever index is contiguous in
 // memory (a wavefront's load covers a few whole cache lines, where loading MFMA operands straight

@@ -237,3 +237,21 @@ def test_weight_gradient_launches_share_partial_tile_lds(monkeypatch):
         assert 160 * 1024 // b == n
     monkeypatch.setenv("ANVIL_HIP_FUSED_WGS", "0")
     assert targets("c4_transformer_t256")[0] == set()
+
+
+def test_layer_norm_folds_into_a_narrow_product(monkeypatch):
+    """hip_rowpro: C4's last layer norm runs in the prologue of the 96-wide output product (three
+    tile columns: 8.5 us against 6.5 + 5.1 for the product and the norm's own launch), while the
+    per-layer norms before y·Wqkv (24 tile columns, each recomputing the rows: 32.5 us against
+    23.1 + 5.1) keep their launch; with the column limit raised all five fold."""
+    src = _source("c4_transformer_t256")
+    labels = _launch_labels(src)
+    fold = [l for l in labels if "layer_norm + layer_norm + layer_norm → matmul" in l]
+    assert len(fold) == 1 and "matmul+add" in fold[0], fold
+    assert src.count("anvil_mm_tile_kpipe_areg<") == 1                  # its one call
+    monkeypatch.setenv("ANVIL_HIP_ROWPRO_COLS", "32")
+    many = _source("c4_transformer_t256")
+    assert many.count("anvil_mm_tile_kpipe_areg<") == 5
+    assert len(_launch_labels(many)) == len(labels) - 4
+    monkeypatch.setenv("ANVIL_HIP_ROWPRO", "0")
+    assert _source("c4_transformer_t256").count("anvil_mm_tile_kpipe_areg<") == 0
