@@ -100,7 +100,10 @@ def im2col_copy(st):
         return None
     strides = ir.row_major_strides([v.extent for v in k.domain])
     want = ir.Affine(0, {v: s for v, s in zip(k.domain, strides) if v.extent > 1})
-    if store.offset != want or store.buf.root.numel != ir.prod(v.extent for v in k.domain):
+    # a variable of extent 1 (C5's single input channel) is always 0, whatever its coefficient
+    got = ir.Affine(store.offset.const, {t: c for t, c in store.offset.terms.items()
+                                         if not (isinstance(t, Var) and t.extent == 1)})
+    if got != want or store.buf.root.numel != ir.prod(v.extent for v in k.domain):
         return None
     loads = ir.loads_in(store.value)
     if len(loads) != 1 or any(not isinstance(t, Var) for t in loads[0].offset.terms):

@@ -160,7 +160,12 @@ def analyse(k: ir.Kernel):
             for which, lin_c, tab_c in (("b", ca, cb), ("a", cb, ca)):
                 lin = _merge(rv, lin_c)
                 K_ = ir.prod(v.extent for v in rv)
-                if lin is not None and abs(lin[1]) == 1 and K_ % 8 == 0 and K_ <= 4096:
+                # (K a multiple of 8 for the matrix cores' 8-k chunks; with $ANVIL_GEMM_SHORT_KTAB=1
+                # also a sum too short for them, which OuterPlan adds up one k at a time: C5's first
+                # convolution, K = 3 x 3, which can then read its input in place of the im2col copy,
+                # and so can its weight gradient; measured 197.2 -> 200.7 us per step, so the copy stays)
+                if (lin is not None and abs(lin[1]) == 1 and (K_ % 8 == 0 or (K_ < MIN_K and os.environ.get("ANVIL_GEMM_SHORT_KTAB", "0") == "1"))
+                        and K_ <= 4096):
                     km = lin
                     steps = [(v.extent, tab_c(v)) for v in lin[0]]
                     ktab = (which, steps)
