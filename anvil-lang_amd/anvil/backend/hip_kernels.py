@@ -891,6 +891,7 @@ class RowsPlan(Plan):
             em.emit(f"{ctype(self._key_dtype(key))} {name}[{Q * self.V}];")
         populated: set = set()
         fwd: dict = {}
+        self.vector_preload(em, sc, populated)
         for si, k in enumerate(self.kernels):
             em.reset_memo()
             cm = self.canon_map(k)
@@ -922,14 +923,19 @@ class RowsPlan(Plan):
                     return st.buf.root.dtype
         return F32
 
-    def element_loop(self, em: Emitter, inner_vars, body_fn):
-        """for q: j = lane + L*q; decode the inner vars; body_fn(q)."""
+    def element_loop(self, em: Emitter, inner_vars, body_fn, after_e=None, before_e=None):
+        """for q: j = lane + L*q; decode the inner vars; body_fn(q). after_e / before_e: called in
+        each q trip once its V elements are done / before they start (cached rows with V > 1 only)."""
         L, Q, n, V = self.L, self.Q, self.n, self.V
         saved_memo = em.memo
         if self.cached:
             em.emit("#pragma unroll")
             em.emit(f"for (int q = 0; q < {Q}; q++) {{")
             em.ind += "    "
+            if V > 1 and before_e is not None:
+                em.memo = dict(saved_memo)
+                before_e()
+                em.memo = saved_memo
             if V > 1:
                 em.emit("#pragma unroll")
                 em.emit(f"for (int e = 0; e < {V}; e++) {{")
@@ -963,6 +969,10 @@ class RowsPlan(Plan):
         if V > 1:
             em.ind = em.ind[:-4]
             em.emit("}")
+            if after_e is not None and self.cached:
+                em.memo = dict(saved_memo)
+                after_e()
+                em.memo = saved_memo
         em.ind = em.ind[:-4]
         em.emit("}")
 
@@ -1008,7 +1018,10 @@ class RowsPlan(Plan):
                 em.emit(arg_pick(op, val, "(int)j", f"best{si}", f"acc{si}"))
             else:
                 em.emit(f"acc{si} = {red_combine(op, dt, f'acc{si}', val)};")
-        self.element_loop(em, list(red.vars), body)
+        ql = self.quad_loads(em, sc, k, cm, list(red.vars))
+        if ql is not None:
+            sc.fwd.update(ql[1])
+        self.element_loop(em, list(red.vars), body, None, ql[0] if ql else None)
         if self.L == 64:
             if arg:
                 em.emit(f"anvil_wave_arg<{mx}, {T}>(best{si}, acc{si});")
@@ -1078,6 +1091,25 @@ class RowsPlan(Plan):
             return
         sc.rand = f"(row * {self.n}u + j)"
         self.install_cache(sc, cm, fwd, populated, em)
+        vec = self.vector_stores(k, cm, inner)
+        self.skip_stores |= {(k.id, i) for i, _ in vec}
+        ql = self.quad_loads(em, sc, k, cm, inner)
+        if ql is not None:
+            sc.fwd.update(ql[1])
+
+        def after_e():
+            # the V values of each vector store, kept in their cache array, as one 16-byte store
+            self.quad_head(em, inner)
+            for i, st in vec:
+                name = self.cache_arrays[canon_key(st.buf, st.offset, cm)]
+                target = f"{sc.buf(st.buf)}[{em.affine(st.offset, st.buf)}]"
+                vals = ", ".join(f"{name}[q * 4 + {e}]" for e in range(4))
+                em.emit(f"{{ const anvil_f32x4 w_ = {{{vals}}};")
+                if st.buf.root.kind == "output":
+                    em.emit(f"  __builtin_nontemporal_store(w_, (anvil_f32x4 *)&{target}); }}")
+                else:
+                    em.emit(f"  *(anvil_f32x4 *)&{target} = w_; }}")
+            self.quad_tail(em)
 
         def body():
             def on_store(st, val):
@@ -1091,7 +1123,114 @@ class RowsPlan(Plan):
                     sc.fwd[key] = f"{name}[{self.slot}]"
                     self.populated_now.add(key)
             self.statements(em, k, sc, parallel=True, on_store=on_store)
-        self.element_loop(em, inner, body)
+        self.element_loop(em, inner, body, after_e if vec else None, ql[0] if ql else None)
+        self.skip_stores -= {(k.id, i) for i, _ in vec}
+
+    # 16-byte loads and stores of a cached row (V = 4: lane l holds elements 4(l + L·q) .. + 3)
+    @staticmethod
+    def quad_aligned(off, inner_last) -> bool:
+        """Are the 4 elements a lane holds side by side in memory, the first at a multiple of 4
+        (so, buffers being 16-byte aligned, one 16-byte access)?"""
+        if off.gathers() or off.scalars() or off.const % 4 or off.terms.get(inner_last) != 1:
+            return False
+        return all(isinstance(t, Var) and (t is inner_last or c % 4 == 0) for t, c in off.terms.items())
+
+    def quad_enabled(self) -> bool:
+        return self.cached and self.V == 4 and os.environ.get("ANVIL_HIP_VEC_ROWS", "1") != "0"
+
+    def quad_head(self, em, inner):
+        em.emit("{")
+        em.ind += "    "
+        em.emit(f"const uint32_t j = 4u * ((uint32_t)lane + {self.L}u * (uint32_t)q);")
+        if self.n % (self.L * 4):
+            em.emit(f"if (j < {self.n}u) {{")
+            em.ind += "    "
+        for line in decode(inner, "j", "uint32_t"):
+            em.emit(line)
+
+    def quad_tail(self, em):
+        if self.n % (self.L * 4):
+            em.ind = em.ind[:-4]
+            em.emit("}")
+        em.ind = em.ind[:-4]
+        em.emit("}")
+
+    def quad_loads(self, em, sc, k, cm, inner):
+        """A before_e hook for stage k: its loads of buffers the plan does not write, held in no
+        cache array, 4 side by side (a per-column scale or shift), one 16-byte load per lane and q
+        trip; the element loop then reads them from there."""
+        if not self.quad_enabled() or not inner:
+            return None
+        written = {b.id for kk in self.kernels for b in A.kernel_writes(kk)}
+        picks, seen = [], set()
+        for ld in A.kernel_loads(k):
+            b = ld.buf.root
+            key = canon_key(ld.buf, ld.offset, cm)
+            if (key is None or key in seen or key in self.cache_arrays or b.id in written or b.dtype != F32
+                    or not b.shape or not self.quad_aligned(ld.offset, inner[-1])):
+                continue
+            seen.add(key)
+            picks.append((key, ld))
+        if not picks:
+            return None
+        names = {key: f"qv{n}_" for n, (key, _) in enumerate(picks)}
+
+        def hook():
+            em.emit(f"anvil_f32x4 {', '.join(names.values())};")
+            self.quad_head(em, inner)
+            for key, ld in picks:
+                em.emit(f"{names[key]} = *(const anvil_f32x4 *)&{sc.buf(ld.buf)}[{em.affine(ld.offset, ld.buf)}];")
+            self.quad_tail(em)
+        return hook, {key: f"{name}[e]" for key, name in names.items()}
+
+    def vector_stores(self, k, cm, inner):
+        """(index, store) of k's stores that go out 16 bytes at a time: plain f32 stores whose value
+        the row's cache array holds, 4 elements side by side."""
+        if not self.quad_enabled() or not inner:
+            return []
+        out = []
+        for i, st in enumerate(k.stmts):
+            if (not isinstance(st, ir.Store) or st.accumulate or st.buf.dtype != F32 or (k.id, i) in self.skip_stores
+                    or canon_key(st.buf, st.offset, cm) not in self.cache_arrays
+                    or not self.quad_aligned(st.offset, inner[-1])):
+                continue
+            out.append((i, st))
+        return out
+
+    def vector_preload(self, em, sc, populated):
+        """Cached row values of buffers the plan does not write, loaded 16 bytes at a time before the
+        first stage (the stages then read them from the cache)."""
+        if not self.quad_enabled():
+            return
+        written = {b.id for k in self.kernels for b in A.kernel_writes(k)}
+        done: set = set()
+        for k in self.kernels:
+            cm = self.canon_map(k)
+            outer, inner = self.stage_vars(k)
+            if not inner:
+                continue
+            for ld in A.kernel_loads(k):
+                b = ld.buf.root
+                key = canon_key(ld.buf, ld.offset, cm)
+                if (key is None or key in done or key in populated or key not in self.cache_arrays or b.id in written
+                        or b.dtype != F32 or not b.shape or not self.quad_aligned(ld.offset, inner[-1])):
+                    continue
+                done.add(key)
+                for i, v in enumerate(outer):
+                    sc.names[v] = f"v{self.outer[i].id}"
+                name = self.cache_arrays[key]
+                em.reset_memo()
+                em.emit("#pragma unroll")
+                em.emit(f"for (int q = 0; q < {self.Q}; q++) {{")
+                em.ind += "    "
+                self.quad_head(em, inner)
+                em.emit(f"const anvil_f32x4 w_ = *(const anvil_f32x4 *)&{sc.buf(ld.buf)}[{em.affine(ld.offset, ld.buf)}];")
+                em.emit(" ".join(f"{name}[q * 4 + {e}] = w_[{e}];" for e in range(4)))
+                self.quad_tail(em)
+                em.ind = em.ind[:-4]
+                em.emit("}")
+                populated.add(key)
+        em.reset_memo()
 
     def grid(self):
         return self.blocks, self.threads

@@ -255,3 +255,22 @@ def test_layer_norm_folds_into_a_narrow_product(monkeypatch):
     assert len(_launch_labels(many)) == len(labels) - 4
     monkeypatch.setenv("ANVIL_HIP_ROWPRO", "0")
     assert _source("c4_transformer_t256").count("anvil_mm_tile_kpipe_areg<") == 0
+
+
+def test_cached_rows_move_16_bytes_per_lane(monkeypatch):
+    """A row kept in registers (4 elements per lane, side by side and 16-byte aligned) is loaded and
+    stored 16 bytes at a time, and a per-column operand the row does not write (layer norm's γ and
+    β) likewise: C3's softmax over rows of 4096 54.8 -> 40.5 us (61 -> 83 % of HBM), its layer norm
+    11.29 -> 11.09 us. The compiler made separate 4-byte accesses of the element loop."""
+    def kernel(name):
+        prog, data = load_ir(name)
+        src = hip.generate(prog, seed=data.get("seed", 0), library=True)
+        i = src.index("// rows: ")
+        return src[i:src.index("\n}\n", i)]
+    sm = kernel("c3_softmax")
+    assert sm.count("*(const anvil_f32x4 *)&") == 1 and sm.count("__builtin_nontemporal_store(w_") == 1
+    assert "anvil_store_out(" not in sm
+    ln = kernel("c3_layernorm")
+    assert ln.count("*(const anvil_f32x4 *)&") == 3          # x, and γ and β in the last stage
+    monkeypatch.setenv("ANVIL_HIP_VEC_ROWS", "0")
+    assert "anvil_f32x4" not in kernel("c3_softmax")
