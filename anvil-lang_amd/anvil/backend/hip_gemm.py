@@ -610,8 +610,12 @@ class GemmPlan(Plan):
                 break
         nch = -(-(self.kslice // (8 * self.kgroup)) // self.waves)      # chunks per wave
         self.depth = max(1, min(int(os.environ.get("ANVIL_GEMM_DEPTH", "2" if nch <= 32 else "4")), nch))
-        # independent accumulator chains per wavefront when it has one 32 x 32 tile
-        self.chains = int(os.environ.get("ANVIL_GEMM_CHAINS", "1")) if self.ptm * self.ptn == 1 else 1
+        # independent accumulator chains per wavefront when it has one 32 x 32 tile and a long run of
+        # chunks ($ANVIL_GEMM_CHAINS_NCH of them at least). Measured (one MI355X, three runs each): C4 at
+        # T = 256, whose weight gradients run 64 chunks per wavefront, 1386-1387 -> 1382 µs per step;
+        # C5 194.8 -> 194.0-194.1; two chains on the short runs too (C2's batch-256 products) no faster
+        one = self.ptm * self.ptn == 1 and nch >= int(os.environ.get("ANVIL_GEMM_CHAINS_NCH", "32"))
+        self.chains = int(os.environ.get("ANVIL_GEMM_CHAINS", "2")) if one else 1
         self.threads = 64 * self.waves if self.sched == "ksplit" else 256
         self.tm = -(-s.M // self.BM)
         self.tn = -(-s.N // self.BN)
