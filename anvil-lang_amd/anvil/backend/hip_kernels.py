@@ -345,7 +345,10 @@ class MapPlan(Plan):
 
     def vector_width(self):
         # four consecutive elements per lane and step when every access is unit-stride along the
-        # innermost variable: the compiler merges them into 16-byte loads and stores
+        # innermost variable, or (pairs) when the innermost variable has extent 2 and the one before
+        # it an even extent (a 2-wide window's elements: two windows per lane); the accesses that
+        # the lane's four elements make side by side then go out as one 16-byte (or, shared by two
+        # elements each, 8-byte) access (`vector_accesses`)
         k = self.k
         inner = k.domain[-1] if k.domain else None
         unit = inner is not None and unit_stride(k, inner)
@@ -353,8 +356,74 @@ class MapPlan(Plan):
             for off in [ld.offset for ld in A.kernel_loads(e)] + [st.offset for st in e.stores]:
                 sub = _subst(off, m)
                 unit = unit and sub is not None and sub.coef(inner) in (0, 1)
+        self.pairs = False
         self.V = 4 if (unit and not self.gen.emulate and inner.extent % 4 == 0) else 1
+        if (self.V == 1 and not self.gen.emulate and len(k.domain) >= 2 and inner.extent == 2
+                and k.domain[-2].extent % 2 == 0 and os.environ.get("ANVIL_HIP_MAP_PAIRS", "1") != "0"):
+            self.pairs, self.V = True, 4
+            loads, stores = self.vector_accesses()
+            if not loads and not stores:
+                self.pairs, self.V = False, 1
         self.blocks = max(1, min(-(-self.total // (THREADS * self.V)), MAX_BLOCKS))
+
+    def _vector_kind(self, off) -> str | None:
+        """For an access at `off` (over this kernel's domain variables) by the four elements of a
+        lane: "x4" when they lie side by side from a multiple of 4 (one 16-byte access, buffers
+        being 16-byte aligned), "x2" when pairs of them share each of two adjacent elements from an
+        even one (pairs mode: one 8-byte access), else None."""
+        if off is None or off.gathers() or off.scalars() or any(not isinstance(t, Var) for t in off.terms):
+            return None
+        inner = self.k.domain[-1]
+        lead = {inner}
+        if self.pairs:
+            j = self.k.domain[-2]
+            lead.add(j)
+            steps = tuple((e >> 1) * off.coef(j) + (e & 1) * off.coef(inner) for e in range(4))
+        else:
+            steps = tuple(e * off.coef(inner) for e in range(4))
+
+        def aligned(m):
+            return off.const % m == 0 and all(t in lead or c % m == 0 for t, c in off.terms.items())
+        if steps == (0, 1, 2, 3) and aligned(4):
+            return "x4"
+        if self.pairs and steps == (0, 0, 1, 1) and aligned(2):
+            return "x2"
+        return None
+
+    def vector_accesses(self):
+        """(loads, stores) that the lane's four elements make as one access: loads [(name, kind,
+        load, offset over the lead's variables, [Load nodes it serves])] of f32 buffers the plan does
+        not write; stores {id(store): (name, store, offset)}, plain f32 stores of buffers no load of
+        the plan reads (they leave after the lane's four elements are computed)."""
+        if self.V != 4 or self.gen.check or os.environ.get("ANVIL_HIP_VEC_MAP", "1") == "0":
+            return [], {}
+        parts = [(self.k, None)] + [(e, m) for e, m, _ in self.followers]
+        written = {b.id for p, _ in parts for b in A.kernel_writes(p)}
+        read = set()
+        loads, by_key = [], {}
+        for p, m in parts:
+            for ld in A.kernel_loads(p):
+                b = ld.buf.root
+                read.add(b.id)
+                off = ld.offset if m is None else _subst(ld.offset, m)
+                kind = self._vector_kind(off) if b.dtype == F32 and b.shape and b.id not in written else None
+                if kind is None:
+                    continue
+                key = (b.id, off.key())
+                if key not in by_key:
+                    by_key[key] = len(loads)
+                    loads.append((f"{'qv' if kind == 'x4' else 'pv'}{len(loads)}_", kind, ld, off, []))
+                loads[by_key[key]][4].append(ld)
+        stores = {}
+        for p, m in parts:
+            for i, st in enumerate(p.stmts):
+                if (not isinstance(st, ir.Store) or (p.id, i) in self.skip_stores or st.accumulate
+                        or st.buf.root.dtype != F32 or st.buf.root.id in read):
+                    continue
+                off = st.offset if m is None else _subst(st.offset, m)
+                if self._vector_kind(off) == "x4":
+                    stores[id(st)] = (f"sv{len(stores)}_", st, off, (p.id, i))
+        return loads, stores
 
     def absorb(self, e, how):
         """Take elementwise kernel e as a follower (how: its var map and forwarded loads, from
@@ -378,11 +447,23 @@ class MapPlan(Plan):
         body: list[str] = []
         ind = "        " if self.V == 1 else "            "
         em = Emitter(sc, body, ind)
+        vloads, vstores = self.vector_accesses()
+        picks = {id(ld): f"{name}[e]" if kind == "x4" else f"{name}[e >> 1]"
+                 for name, kind, _, _, served in vloads for ld in served}
+        if picks:
+            def override(x, sc=sc):
+                got = picks.get(id(x))
+                return got if got is not None else KernelScope.override_load(sc, x)
+            sc.override_load = override
+        deferred = {key for _, _, _, key in vstores.values()}
+        self.skip_stores |= deferred
         for line in decode(k.domain, "u", it):
             em.emit(line)
         stored = {}
 
         def on_store(st, val):
+            if id(st) in vstores:
+                em.emit(f"{vstores[id(st)][0]}[e] = {val};")
             if not st.accumulate:
                 stored[st.buf.root.id] = val
         self.statements(em, k, sc, parallel=True, on_store=on_store)
@@ -395,16 +476,45 @@ class MapPlan(Plan):
             sc.fwd = {canon_key(ld.buf, ld.offset, canon): stored[ld.buf.root.id] for ld in fwd}
             self.statements(em, e, sc, parallel=True, on_store=on_store)
             sc.canon, sc.fwd = None, {}
+        self.skip_stores -= deferred
         n = self.total // self.V
-        head = [self.comment() + (f" · {self.V} elements per lane" if self.V > 1 else ""), self.header(self.threads),
+        what = (" · two 2-wide windows (4 elements) per lane" if self.pairs else
+                f" · {self.V} elements per lane" if self.V > 1 else "")
+        if vloads or vstores:
+            what += f", {len(vloads)} loads and {len(vstores)} stores as one access each"
+        pre: list[str] = []
+        tail: list[str] = []
+        if vloads or vstores:
+            # the lane's first element's variables, for the wide accesses' addresses
+            pem = Emitter(sc, pre, "            ")
+            pem.emit(f"const {it} u = {self.V}u * w;")
+            for line in decode(k.domain, "u", it):
+                pem.emit(line)
+            for name, kind, ld, off, _ in vloads:
+                T = "anvil_f32x4" if kind == "x4" else "anvil_f32x2"
+                pem.emit(f"const {T} {name} = *(const {T} *)&{sc.buf(ld.buf)}[{pem.affine(off, ld.buf)}];")
+            if vstores:
+                pem.emit(f"anvil_f32x4 {', '.join(v[0] for v in vstores.values())};")
+            pre.insert(0, "        {")
+            post: list[str] = []
+            tem = Emitter(sc, post, "            ")
+            for name, st, off, _ in vstores.values():
+                target = f"{sc.buf(st.buf)}[{tem.affine(off, st.buf)}]"
+                if st.buf.root.kind == "output":
+                    tem.emit(f"__builtin_nontemporal_store({name}, (anvil_f32x4 *)&{target});")
+                else:
+                    tem.emit(f"*(anvil_f32x4 *)&{target} = {name};")
+            tail = post + ["        }"]
+        # (the header last: the buffers the kernel takes are known once every access is emitted)
+        head = [self.comment() + what, self.header(self.threads),
                 f"    for ({it} w = ({it})blockIdx.x * {self.threads}u + threadIdx.x; w < {n}u; "
                 f"w += ({it})gridDim.x * {self.threads}u) {{"]
         if self.V == 1:
             head.append("        const auto u = w;")
             return "\n".join(head + body + ["    }", "}"])
-        head += ["#pragma unroll", f"        for ({it} e = 0; e < {self.V}u; e++) {{",
+        head += pre + ["#pragma unroll", f"        for ({it} e = 0; e < {self.V}u; e++) {{",
                  f"            const {it} u = {self.V}u * w + e;"]
-        return "\n".join(head + body + ["        }", "    }", "}"])
+        return "\n".join(head + body + ["        }"] + tail + ["    }", "}"])
 
     def grid(self):
         return self.blocks, self.threads

@@ -22,6 +22,7 @@
 
 typedef float anvil_f32x16 __attribute__((ext_vector_type(16)));
 typedef float anvil_f32x4 __attribute__((ext_vector_type(4)));
+typedef float anvil_f32x2 __attribute__((ext_vector_type(2)));
 
 #ifndef ANVIL_MM_BK
 #define ANVIL_MM_BK 16       // k depth of the LDS-staged tile schedule's slices

@@ -287,3 +287,30 @@ def test_max_pool_takes_two_outputs_per_lane(monkeypatch):
     assert "589824 pairs" in kern                       # 128 x 64 x 12 x 12 outputs, in pairs
     monkeypatch.setenv("ANVIL_HIP_POOL", "0")
     assert "two outputs of the 2-wide window" not in _source("c5_cnn")
+
+
+def test_max_pool_gradient_takes_two_windows_per_lane(monkeypatch):
+    """C5's max-pool gradient (then ReLU's) as a map over [n·c·i, u, j, v] with v of extent 2: each
+    lane takes two windows' elements along j (four elements), the pre-pool activations in one
+    16-byte load, the pooled values and their gradient in one 8-byte load each (shared by the two
+    elements of a window), and the result in one 16-byte store; each element's value is the same
+    expression as before, so the results are the same bits."""
+    src = _source("c5_cnn")
+    i = src.index("two 2-wide windows (4 elements) per lane")
+    kern = src[i:src.index("\n}\n", i)]
+    assert kern.count("*(const anvil_f32x4 *)&") == 1 and kern.count("*(const anvil_f32x2 *)&") == 2
+    assert kern.count("*(anvil_f32x4 *)&") == 1 and "w < 1179648u" in kern      # 4718592 elements / 4
+    assert "[e >> 1]" in kern and "[e]" in kern
+    monkeypatch.setenv("ANVIL_HIP_MAP_PAIRS", "0")
+    assert "two 2-wide windows" not in _source("c5_cnn")
+
+
+def test_four_element_maps_access_16_bytes_at_a_time(monkeypatch):
+    """A map with four consecutive elements per lane loads and stores the side-by-side ones as one
+    16-byte access each (C4's embedding sum: the positional table row) instead of four 4-byte
+    ones that the compiler leaves unmerged."""
+    src = _source("c4_transformer_t256")
+    heads = [l for l in src.split("\n") if l.startswith("// map:") and "4 elements per lane, 1 loads and 1 stores" in l]
+    assert heads
+    monkeypatch.setenv("ANVIL_HIP_VEC_MAP", "0")
+    assert "stores as one access each" not in _source("c4_transformer_t256")
