@@ -283,6 +283,52 @@ def _offset_fn(vs, coef, src: str) -> str:
     return " + ".join(parts) or "0LL"
 
 
+# the largest operand copied for an input gradient (floats): a copy of at most 1 MB beside the launch
+# before the product
+PACK_MAX = 1 << 18
+
+
+class PackPlan(Plan):
+    """The first operand of an input gradient's product copied in the order the product reads it:
+    dst[t, k] = W[row(t) + k(k)], t over the product's rows (the input channels), k over (u, v, o)
+    in the product's k order. It runs in the launch before the product (side by side with it when
+    that launch does not write W, else alone), so it copies W as the product would have read it."""
+
+    kind = "pack"
+
+    def __init__(self, gen, dgrad, src, dst, off2):
+        super().__init__(gen, [], f"k{dgrad.G.id}p")
+        self.dgrad, self.src, self.dst, self.off2 = dgrad, src, dst, off2
+        self.total = dgrad.M * dgrad.K
+        self.threads = 256
+        self.label = f"operand copy: {dgrad.G.name}'s weights in k order"
+
+    def with_threads(self, threads):
+        """The same copy with `threads` lanes per workgroup (to run beside a launch of that size)."""
+        q = PackPlan(self.gen, self.dgrad, self.src, self.dst, self.off2)
+        q.threads = threads
+        return q
+
+    def grid(self):
+        from .hip_kernels import MAX_BLOCKS
+        return max(1, min(-(-self.total // self.threads), MAX_BLOCKS)), self.threads
+
+    def source(self) -> str:
+        d, off2 = self.dgrad, self.off2
+        row = _offset_fn(d.rows[0], off2.coef, "t")
+        kof = _offset_fn(d.korder, off2.coef, "k")
+        t = self.threads
+        return "\n".join([
+            f"// pack: the weights of {d.G.name} as rows of its {d.K} k · {d.M}x{d.K}",
+            self.header(t),
+            f"    for (uint32_t w = (uint32_t)blockIdx.x * {t}u + threadIdx.x; w < {self.total}u; "
+            f"w += (uint32_t)gridDim.x * {t}u) {{",
+            f"        const uint32_t t = w / {d.K}u, k = w % {d.K}u;",
+            f"        {self.use_buf(self.dst)}[w] = {self.use_buf(self.src.root)}[{off2.const}LL + {row} + {kof}];",
+            "    }",
+            "}"])
+
+
 def match_dgrad(gen, stmts: list, i: int):
     """(DgradPlan, statements it takes) for a product that fills im2col-shaped gradients
     dP[n, i, j, c, u, v] = Σ_o dY[n, o, i, j]·W[o, c, u, v], an optional zero fill of dX, and the
@@ -466,6 +512,21 @@ class DgradPlan(Plan):
         depth = int(os.environ.get("ANVIL_DGRAD_DEPTH", "0")) or (2 if nch <= 32 else 4)
         self.kg, self.nch, self.depth = kg, nch, min(depth, nch)
         self.follower, self.fwd, self.dx_dead = None, [], False
+        self.pack = self.make_pack()
+
+    def make_pack(self):
+        """A PackPlan for the first operand (the weights, W[o, c, u, v] read as A[c, (u, v, o)]:
+        each lane's four consecutive k lie 288 floats apart and the lanes 9 apart) when it is an
+        f32 buffer read without a window check and small: the product then reads 4 consecutive k
+        with one 16-byte load from the packed copy A[c, k] (a timing copy with the rows read that
+        way: C5 192 -> 185 us per step). $ANVIL_DGRAD_PACK=0 reads the weights in place."""
+        e, ld, off1, off2 = self.ops[0]
+        b = ld.buf.root
+        if (os.environ.get("ANVIL_DGRAD_PACK", "1") == "0" or self.side_pred[0] or b.dtype != "f32"
+                or self.K % 4 or self.M * self.K > PACK_MAX or off2.gathers() or off2.scalars()):
+            return None
+        buf = A.new_buffer(self.gen.ids.take(), f"{b.name}.packed", (self.M, self.K), "f32", "scratch")
+        return PackPlan(self.gen, self, ld.buf, buf, off2)
 
     def follow(self, e, fwd):
         """Run elementwise kernel e (which reads dX only at its own element) on each dX element as
@@ -511,6 +572,12 @@ class DgradPlan(Plan):
         body += [f"    const int m0 = blockIdx.y * {32 * TM}, n0 = blockIdx.x * {32 * TN};"]
         for n in (0, 1):
             e, ld, off1, off2 = self.ops[n]
+            if n == 0 and self.pack is not None:                 # row t of the packed copy: K floats
+                body += [f"    const float *pa = {sc.buf(self.pack.dst)};",
+                         f"    auto arow = [=](int t) -> long long {{ return {self.K}LL * (long long)(uint32_t)(t); }};",
+                         "    auto ak = [=](int k) -> long long { return (long long)(uint32_t)(k); };",
+                         "    anvil_all_pred apred;"]
+                continue
             body.append(f"    const float *p{names[n]} = {sc.buf(ld.buf)} + ({off2.const}LL);")
             body.append(f"    auto {names[n]}row = [=](int t) -> long long {{ return "
                         f"{_offset_fn(self.rows[n], off2.coef, 't')}; }};")
@@ -528,6 +595,9 @@ class DgradPlan(Plan):
                 body.append(f"    anvil_all_pred {names[n]}pred;")
         inner = self.korder[-1]
         a_ks, b_ks = self.ops[0][3].coef(inner), self.ops[1][3].coef(inner)
+        amode = "ANVIL_LD_ANY"
+        if self.pack is not None:
+            a_ks, amode = 1, "ANVIL_LD_KC"
         chk = lambda x, t: "true" if x % t else "false"
         per = 16 // W
         # the follower's other loads (ReLU's z at the element) are issued before the product
@@ -561,7 +631,7 @@ class DgradPlan(Plan):
             body += pl + ["    }"]
         body += [f"    __shared__ float anvil_kp_lds[{W * TM * TN * 16 * 64}];",
                  f"    float part[{TM}][{TN}][{per}];",
-                 f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, ANVIL_LD_ANY, ANVIL_LD_ANY, {self.nch}, {self.depth}, "
+                 f"    anvil_mm_tile_kpipe<{W}, {TM}, {TN}, {amode}, ANVIL_LD_ANY, {self.nch}, {self.depth}, "
                  f"{chk(self.M, 32 * TM)}, {chk(self.N, 32 * TN)}, {self.kg}>(anvil_kp_lds, part, pa, arow, ak, {a_ks}LL, pb, brow, bk, "
                  f"{b_ks}LL, {self.M}, {self.N}, m0, n0, 0, {self.K}, opa, opb, apred, bpred);"]
         if not hoisted:
@@ -593,6 +663,7 @@ class DgradPlan(Plan):
             body += lines
         body.append("    }")
         head = [f"// conv-dgrad: {self.G.name} (product into an im2col-shaped gradient) and {self.S.name} (its "
-                f"scatter) as one product · {self.M}x{self.N}x{self.K}, window terms over the edge skipped",
+                f"scatter) as one product · {self.M}x{self.N}x{self.K}, window terms over the edge skipped"
+                + (f", the weights from their packed copy ({self.pack.name})" if self.pack is not None else ""),
                 self.header(64 * W)]
         return "\n".join(head + body + ["}"])

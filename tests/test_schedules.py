@@ -314,3 +314,39 @@ def test_four_element_maps_access_16_bytes_at_a_time(monkeypatch):
     assert heads
     monkeypatch.setenv("ANVIL_HIP_VEC_MAP", "0")
     assert "stores as one access each" not in _source("c4_transformer_t256")
+
+
+def test_input_gradient_reads_a_packed_copy_of_the_weights(monkeypatch):
+    """C5's input gradient reads W2[o, c, u, v] as A[c, (u, v, o)]; a copy packed in that order
+    (32 x 576 floats) is written in the launch before it (beside the max-pool gradient, which does
+    not write W2), and the product reads 4 consecutive k with one 16-byte load (ANVIL_LD_KC)."""
+    src = _source("c5_cnn")
+    assert "// fused: k26278, k26305p side by side" in src
+    i = src.index("// conv-dgrad: k26305")
+    kern = src[i:src.index("\n}\n", i)]
+    assert "the weights from their packed copy (k26305p)" in kern
+    assert "anvil_mm_tile_kpipe<4, 1, 2, ANVIL_LD_KC, ANVIL_LD_ANY" in kern
+    assert "576LL * (long long)(uint32_t)(t)" in kern
+    labels = _launch_labels(src)
+    at = next(n for n, l in enumerate(labels) if "k26305p pack" in l)
+    assert labels[at + 1] == "∂forward + zero + ∂forward + ∂max" and "∂max_pool2d" in labels[at]
+    monkeypatch.setenv("ANVIL_DGRAD_PACK", "0")
+    assert "k26305p" not in _source("c5_cnn")
+
+
+def test_a_pack_runs_alone_after_a_launch_that_writes_its_weights():
+    """When the launch before the input gradient writes the weights, the packed copy cannot run
+    beside it (it would read them before that launch's writes): it takes a launch of its own."""
+    import types
+    prog, data = load_ir("c5_cnn")
+    g = hip.HipGen(prog, seed=data.get("seed", 0))
+    W = prog.buffers[0]
+    # the launch before: a map that writes W; the copy reads W
+    writer = types.SimpleNamespace(kind="map", grid=lambda: (1, 256), kernels=[ir.Kernel(
+        [ir.Var("i", 4)], [ir.Store(W, ir.Affine(0, {}), ir.Const(0.0))], name="w")])
+    pack = types.SimpleNamespace(src=W)
+    pack.with_threads = lambda t: pack
+    g.plans, seg = [writer], [("launch", [], writer)]
+    g.launch = lambda p, ind: []
+    g.place_pack(pack, seg, "")
+    assert pack.own is pack and g.plans == [writer, pack] and seg[-1][2] is pack
