@@ -976,11 +976,35 @@ class GemmPlan(Plan):
                     + (f" · K over {len(s.k_multi)} variables" if s.k_multi else ""),
                     self.header(self.threads)]
         if self.kslices > 1:
-            # partial tiles only: GemmReducePlan adds them up and runs the epilogue
+            # partial tiles: GemmReducePlan adds them up and runs the epilogue, or (fixup) the last
+            # workgroup of each tile to finish does, here
             ws = sc.buf(self.ws_buffer())
             store = loop + [f"        {ws}[(((long long)slice * {s.B} + bz) * {s.M} + mi) * {s.N} + ni] = {value};",
                             "    }"]
-            return "\n".join(head() + body + main + store + ["}"])
+            if not getattr(self, "fixup", False):
+                return "\n".join(head() + body + main + store + ["}"])
+            S, cnt = self.kslices, f"anvil_cnt_{self.name}"
+            fix = ["    // the tile's last workgroup to finish (its S partial tiles stored, made visible device-wide",
+                   "    // before the count) adds them in slice order and runs the epilogue: the sum of the",
+                   "    // partial-tile launch, without that launch; it sets the count back to 0 for the next one",
+                   "    __shared__ int anvil_last_;",
+                   f"    const int tile_ = ((int)bz * {self.tm} + m0 / {self.BM}) * {self.tn} + n0 / {self.BN};",
+                   "    __threadfence();",
+                   "    __syncthreads();",
+                   f"    if (threadIdx.x == 0) anvil_last_ = atomicAdd(&{cnt}[tile_], 1u) == {S - 1}u;",
+                   "    __syncthreads();",
+                   "    if (!anvil_last_) return;",
+                   "    __threadfence();",
+                   "    auto fx_ = [&](int mi, int ni) -> float {",
+                   "        float sum = 0.0f;",
+                   f"        for (int sl = 0; sl < {S}; sl++) sum += {ws}[(((long long)sl * {s.B} + bz) * {s.M} + mi) * {s.N} + ni];",
+                   "        return sum;",
+                   "    };"]
+            _, post = self.epilogue(sc, loop, slot, "fx_(mi, ni)", [], per)
+            tail = [f"    if (threadIdx.x == 0) {cnt}[tile_] = 0u;"]
+            decl = f"static __device__ unsigned {cnt}[{self.tn * self.tm * s.B}];   // finished slices per tile\n"
+            text = "\n".join(head() + body + main + store + fix + post + tail + ["}"])
+            return decl + text
         hoisted = []
         if per * 4 <= 64 and os.environ.get("ANVIL_GEMM_HOIST", "1") != "0":
             hoisted = self.hoistable([(k, None, [])] + list(self.followers))[:max(0, 64 // per)]

@@ -143,13 +143,23 @@ def _launch_labels(src):
 def test_a_second_launch_joins_the_next_independent_launch():
     """The partial-tile sum of a K split runs side by side with the next launch when no data passes
     between them: the first launch holds the product and seven maps (eight parts at most), the
-    eighth map then shares the sum's launch. A kernel that reads the product keeps the sum alone."""
+    eighth map then shares the sum's launch. When a kernel reads the product, the sum cannot join
+    that launch and stays alone (or, with ANVIL_GEMM_FIXUP=1, the product's last workgroup per tile
+    adds the partial tiles)."""
     labels = _launch_labels(hip.generate(_split_product_then_nine(False)))
     assert labels[0].startswith("k") and labels[0].count(" map: ") == 7 and " gemm: g" in labels[0]
     assert " map: e7 | " in labels[1] and "gemm-reduce: partial-tile sum + g" in labels[1], labels
     labels = _launch_labels(hip.generate(_split_product_then_nine(True)))
     assert labels[1] == "partial-tile sum + g", labels
     assert "map: e7" in labels[2] and "map: t" in labels[2]
+    os.environ["ANVIL_GEMM_FIXUP"] = "1"
+    try:
+        src = hip.generate(_split_product_then_nine(True))
+    finally:
+        del os.environ["ANVIL_GEMM_FIXUP"]
+    labels = _launch_labels(src)
+    assert len(labels) == 2 and "map: e7" in labels[1] and "map: t" in labels[1], labels
+    assert "anvil_last_" in src and "gemm-reduce" not in src
 
 
 def test_c4_and_c5_weight_update_sums_join_the_next_launch(monkeypatch):
@@ -350,3 +360,21 @@ def test_a_pack_runs_alone_after_a_launch_that_writes_its_weights():
     g.launch = lambda p, ind: []
     g.place_pack(pack, seg, "")
     assert pack.own is pack and g.plans == [writer, pack] and seg[-1][2] is pack
+
+
+def test_a_lone_k_split_adds_its_partial_tiles_in_its_last_workgroup(monkeypatch):
+    """With ANVIL_GEMM_FIXUP=1, a K split whose partial-tile sum cannot join the next launch (C5's
+    first fully connected product: the row block after it reads its result; C4's 256 x 96 x 4096
+    weight gradient, in a launch with three other products) adds the partial tiles in the last
+    workgroup of each tile to finish, in slice order, instead of in a second launch; the count of
+    finished slices per tile is set back to zero by that workgroup. (Off by default: slower.)"""
+    assert "anvil_cnt_" not in _source("c5_cnn")
+    monkeypatch.setenv("ANVIL_GEMM_FIXUP", "1")
+    src = _source("c5_cnn")
+    assert "static __device__ unsigned anvil_cnt_k26677[16];" in src
+    assert "atomicAdd(&anvil_cnt_k26677[tile_], 1u) == 17u" in src and "anvil_cnt_k26677[tile_] = 0u;" in src
+    assert "k26677r" not in src and "for (int sl = 0; sl < 18; sl++)" in src
+    src4 = _source("c4_transformer_t256")
+    assert "anvil_cnt_k25543[24]" in src4 and "k25543r" not in src4
+    monkeypatch.setenv("ANVIL_GEMM_FIXUP", "0")
+    assert "// gemm-reduce: k26677" in _source("c5_cnn")
