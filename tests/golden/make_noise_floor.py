@@ -9,9 +9,10 @@ with the reference's own (tests/golden/vectors/<name>.npz). The spread it record
 correct float32 implementation that sums in its own order can be expected to show; the GPU tests
 hold the HIP libraries to it.
 
-Usage: python tests/golden/make_noise_floor.py [NAME ...]
-  (C2: about 25 minutes on 4 cores; C4 and C5 whole: about 3 hours. Named runs are added to the
-  existing file. A run whose reference vectors make_fixtures.py is still writing waits for them.)
+Usage: python tests/golden/make_noise_floor.py [--orders reversed[,sequential]] [NAME ...]
+  (C2: about 25 minutes on 4 cores; C4 and C5 whole: about 3 hours reversed, longer sequential.
+  Named runs are added to the existing file, each order as soon as it finishes. A run whose
+  reference vectors make_fixtures.py is still writing waits for them.)
 """
 from __future__ import annotations
 
@@ -21,7 +22,7 @@ import os
 import re
 import sys
 import time
-from concurrent.futures import ProcessPoolExecutor
+from concurrent.futures import ProcessPoolExecutor, as_completed
 
 import numpy as np
 
@@ -73,25 +74,40 @@ def one(job):
     return name, steps, lr, order, res
 
 
-def main():
-    only = set(sys.argv[1:])
+ABOUT = ("per kept parameter: |oracle run with the float sums reordered - reference| over "
+         "lr·steps (lr_*) and over the tensor's largest |value| (max_*); losses: each printed "
+         "loss's |reordered - reference| / |reference|; written by tests/golden/make_noise_floor.py")
+
+
+def record(name, steps, lr, order, res, fresh):
+    """Merge one finished run into the file (re-read, so runs finishing elsewhere are kept)."""
     out = {}
-    if only and os.path.exists(OUT):
+    if os.path.exists(OUT):
         with open(OUT) as f:
             out = json.load(f)
-    out["about"] = ("per kept parameter: |oracle run with the float sums reordered - reference| over "
-                    "lr·steps (lr_*) and over the tensor's largest |value| (max_*); losses: each printed "
-                    "loss's |reordered - reference| / |reference|; written by tests/golden/make_noise_floor.py")
-    jobs = [(n, s, lr, o) for n, s, lr in RUNS for o in ORDERS if not only or n in only]
-    for n in {j[0] for j in jobs}:
-        out.pop(n, None)
-    with ProcessPoolExecutor(max_workers=len(jobs)) as pool:
-        for name, steps, lr, order, res in pool.map(one, jobs):
-            out.setdefault(name, {"steps": steps, "lr": lr, "orders": {}})["orders"][order] = res
+    out["about"] = ABOUT
+    if name in fresh:                                    # this invocation's first result for name
+        out.pop(name, None)
+        fresh.discard(name)
+    out.setdefault(name, {"steps": steps, "lr": lr, "orders": {}})["orders"][order] = res
     with open(OUT, "w") as f:
         json.dump(out, f, indent=1, sort_keys=True)
         f.write("\n")
-    print("wrote", OUT)
+    print("wrote", name, order, "to", OUT, flush=True)
+
+
+def main():
+    args = sys.argv[1:]
+    orders = ORDERS
+    if args[:1] == ["--orders"]:
+        orders, args = tuple(args[1].split(",")), args[2:]
+    only = set(args)
+    jobs = [(n, s, lr, o) for n, s, lr in RUNS for o in orders if not only or n in only]
+    # a name's old entry goes when its first run here finishes, unless only some orders are rerun
+    fresh = {j[0] for j in jobs} if orders == ORDERS else set()
+    with ProcessPoolExecutor(max_workers=len(jobs)) as pool:
+        for fut in as_completed([pool.submit(one, j) for j in jobs]):
+            record(*fut.result(), fresh)
 
 
 if __name__ == "__main__":
