@@ -2034,6 +2034,16 @@ class RowBlockPlan(Plan):
                 em.emit(f"if ({guard}) {line}" if guard else line)
             em.reset_memo()
 
+    def wave_only(self, si: int) -> bool:
+        """Does stage si run on the first wavefront's lanes alone (one lane per element, at most
+        64 of them: a row's 10 logits, its one loss)? Only with $ANVIL_ROWBLOCK_WAVESYNC=1: the
+        wave-level fences between such stages measured no faster than the workgroup barriers (C2
+        53.2 -> 53.0 us per step, C5 184.3 -> 185.0)."""
+        if si >= len(self.stages) or os.environ.get("ANVIL_ROWBLOCK_WAVESYNC", "0") != "1":
+            return False
+        st = self.stages[si]
+        return st.form not in ("block", "wave") and st.N <= 64
+
     def lane_loop(self, em, st: RowStage, var: str, stride: int, start: str = "threadIdx.x") -> None:
         """The loop of a lane over its share of the stage's index (`var` < N, in steps of stride);
         with itform, a counted loop (it_) whose trips index the forwarding registers."""
@@ -2106,7 +2116,14 @@ class RowBlockPlan(Plan):
                 self.stage_statements(em, k, sc)
             em.ind = em.ind[:-4]
             em.emit("}")
-            em.emit("__syncthreads();")
+            if self.wave_only(si) and self.wave_only(si + 1):
+                # two stages that only the first wavefront's lanes run: its own lanes' writes are
+                # ordered before its later reads without a workgroup barrier (the other waves meet
+                # the barrier after the last such stage)
+                em.emit("__builtin_amdgcn_fence(__ATOMIC_RELEASE, \"workgroup\"); __builtin_amdgcn_wave_barrier(); "
+                        "__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"workgroup\");")
+            else:
+                em.emit("__syncthreads();")
         for bid, S in self.shadow.items():
             shared.append(f"    __shared__ {ctype(self.gen.by_id[bid].dtype)} sh{bid}[{S}];")
         prologue = self.row_prologue()          # before the header: its loads add parameters

@@ -378,3 +378,18 @@ def test_a_lone_k_split_adds_its_partial_tiles_in_its_last_workgroup(monkeypatch
     assert "anvil_cnt_k25543[24]" in src4 and "k25543r" not in src4
     monkeypatch.setenv("ANVIL_GEMM_FIXUP", "0")
     assert "// gemm-reduce: k26677" in _source("c5_cnn")
+
+
+def test_row_block_stages_of_the_first_wavefront_skip_the_workgroup_barrier(monkeypatch):
+    """With ANVIL_ROWBLOCK_WAVESYNC=1, C2's row block (logits, log-softmax, the loss and their
+    gradients over 256 rows of 10): the stages that run on at most 64 lanes (one per logit or per
+    row) follow each other with a wave-level fence instead of a workgroup barrier; the barrier
+    stays before and after them. (Off by default: no faster.)"""
+    def barriers(src):
+        i = src.index("// rowblock: k1002")
+        kern = src[i:src.index("\n}\n", i)]
+        return kern.count("__syncthreads();"), kern.count("__builtin_amdgcn_wave_barrier();")
+    sync, wave = barriers(_source("c2_full"))
+    assert wave == 0
+    monkeypatch.setenv("ANVIL_ROWBLOCK_WAVESYNC", "1")
+    assert barriers(_source("c2_full")) == (sync - 6, 6)
